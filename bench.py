@@ -1,0 +1,324 @@
+"""Benchmark: fused Q4 decode attention on one MI355X.
+
+Default workload (Llama-3-8B-shape GQA, the headline metric): 8 independent
+caches (8 concurrent sequences), 32 layers, 32 q heads / 8 kv heads, d=128,
+32K context.  One step = append one new token to every sequence (all layers,
+K and V, one batched quantize launch), then fused attention over the full
+32768-token context for every layer (one launch per layer covering all 8
+sequences), then O(1) restore to 32767 tokens so every step sees the same
+context.  Inputs are synthetic, seeded, generated on the device; the caches
+and queries are resident in HBM before the timed region starts.
+
+Prints ONE JSON line.  `value` is the whole step time per layer (µs);
+`roofline` is the fused attention launch: algorithmic bytes (K and V Q4 read
+once: 160 B per token-head at d=128, plus q in and out) over its average
+duration from HIP events on its stream.  `cpu_baseline` is the CPU oracle's
+two-pass fused attention (oracle/eakv_oracle.c) on a bounded sample of the
+same workload, run on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+SEED_BASE = 0xEA4B
+
+# name, layers, q heads, kv heads, d, context, sequences, K dist, V dist
+CONFIGS = {
+    1: dict(name="mha-8h-d128-2k", nl=1, nq=8, nkv=8, d=128, L=2048, nseq=1,
+            k="normal", v="normal"),
+    2: dict(name="tinyllama-gqa8-d64-4k", nl=22, nq=32, nkv=4, d=64, L=4096, nseq=1,
+            k="chan", v="normal"),
+    3: dict(name="llama2-7b-mha-d128-8k", nl=32, nq=32, nkv=32, d=128, L=8192, nseq=1,
+            k="drift", v="drift"),
+    4: dict(name="llama3-8b-gqa4-d128-32k-x8", nl=32, nq=32, nkv=8, d=128, L=32768,
+            nseq=8, k="chan", v="normal"),
+    5: dict(name="70b-gqa8-d128-128k", nl=80, nq=64, nkv=8, d=128, L=131072, nseq=1,
+            k="chan_outlier", v="chan_outlier"),
+}
+
+
+class Synth:
+    """ctypes front of eakv_amd/libeakv_synth.so."""
+
+    class Params(C.Structure):
+        _fields_ = [("seed", C.c_uint64), ("row0", C.c_int64), ("pos0", C.c_int64),
+                    ("sigma", C.c_float), ("chan", C.c_void_p),
+                    ("drift_amp", C.c_float), ("drift_period", C.c_float),
+                    ("outlier_p", C.c_float), ("outlier_v", C.c_float)]
+
+    def __init__(self):
+        self.lib = C.CDLL(os.path.join(ROOT, "eakv_amd", "libeakv_synth.so"))
+        self.lib.eakv_synth_fill.restype = C.c_int
+        self.lib.eakv_synth_fill.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int,
+                                             C.POINTER(self.Params), C.c_void_p]
+
+    def fill(self, ptr, n_rows, n_tok, d, seed, row0, pos0, kind, chan_ptr=None,
+             stream=None):
+        p = self.Params(seed=seed, row0=row0, pos0=pos0, sigma=1.0, chan=None,
+                        drift_amp=0.0, drift_period=512.0, outlier_p=0.0, outlier_v=0.0)
+        if kind in ("chan", "chan_outlier"):
+            p.chan = chan_ptr
+        if kind == "chan_outlier":
+            p.outlier_p, p.outlier_v = 0.01, 20.0
+        if kind == "drift":
+            p.sigma, p.drift_amp = 1.5, 0.1
+        rc = self.lib.eakv_synth_fill(ptr, n_rows, n_tok, d, C.byref(p), stream)
+        if rc:
+            raise RuntimeError(f"synth launch failed: {rc}")
+
+
+def channel_scales(cfg, seed):
+    """Per (sequence, layer, kv, head, dim) K/V channel multipliers (host)."""
+    rng = np.random.default_rng(seed)
+    nseq, nl, nkv, d = cfg["nseq"], cfg["nl"], cfg["nkv"], cfg["d"]
+    ch = np.ones((nseq, nl, 2, nkv, d), np.float32)
+    for kv, kind in ((0, cfg["k"]), (1, cfg["v"])):
+        if kind == "chan":
+            ch[:, :, kv] = np.exp(rng.uniform(np.log(0.5), np.log(4.0), (nseq, nl, nkv, d)))
+            for s in range(nseq):
+                for l in range(nl):
+                    for h in range(nkv):
+                        ch[s, l, kv, h, rng.choice(d, 2, replace=False)] *= 10.0
+        elif kind == "chan_outlier":
+            ch[:, :, kv] = np.exp(rng.uniform(np.log(0.25), np.log(8.0), (nseq, nl, nkv, d)))
+    return ch
+
+
+class Workload:
+    def __init__(self, cfg_id, ctx=None):
+        import eakv_amd as E
+        from eakv_amd import hipmem as H
+        self.E, self.H = E, H
+        self.cfg = dict(CONFIGS[cfg_id])
+        if ctx:
+            self.cfg["L"] = ctx
+        c = self.cfg
+        self.seed = SEED_BASE + cfg_id
+        self.L0 = c["L"] - 1                     # each step appends token L-1
+        self.lmax = c["L"] + 64
+        self.synth = Synth()
+        self.caches = [E.Cache(c["nl"], c["nkv"], c["d"], self.lmax) for _ in range(c["nseq"])]
+        self.handles = E.handles(self.caches)
+        self.stream = self.caches[0].stream
+        self.chan = H.DeviceArray.from_host(channel_scales(c, self.seed))
+        self.out = H.DeviceArray((c["nseq"], c["nq"], c["d"]))
+        self.tok = H.DeviceArray((c["nseq"], c["nl"], 2, c["nkv"], 1, c["d"]))
+        self.quant_ms = None
+
+    def row0(self, s, layer, kv):
+        c = self.cfg
+        return ((s * c["nl"] + layer) * 2 + kv) * c["nkv"]
+
+    def fill_context(self, time_quantize=True):
+        """Synthesize and quantize L0 tokens per layer of every sequence; the
+        quantize launches are timed with events."""
+        E, H, c = self.E, self.H, self.cfg
+        slab = H.DeviceArray((2, c["nkv"], self.L0, c["d"]))
+        half = c["nkv"] * self.L0 * c["d"] * 4
+        ev0, ev1 = H.Event(), H.Event()
+        qtime = 0.0
+        for s, cache in enumerate(self.caches):
+            cache.clear()
+            for l in range(c["nl"]):
+                for kv, kind in ((0, c["k"]), (1, c["v"])):
+                    r0 = self.row0(s, l, kv)
+                    self.synth.fill(slab.ptr + kv * half, c["nkv"], self.L0, c["d"],
+                                    self.seed, r0, 0, kind,
+                                    self.chan.ptr + r0 * c["d"] * 4, self.stream)
+                ev0.record(self.stream)
+                for kv in (0, 1):
+                    rc = E.lib().eakv_cache_append_device(cache.h, slab.ptr + kv * half, l, kv,
+                                                          self.L0, self.stream)
+                    assert rc == 0, E.last_error()
+                ev1.record(self.stream)
+                ev1.synchronize()
+                qtime += ev0.elapsed_ms(ev1)
+            cache.advance(self.L0)
+        slab.free()
+        self.quant_ms = qtime
+        self.quant_bytes = (c["nseq"] * c["nl"] * 2 * c["nkv"] * self.L0 * c["d"]) * (4 + 0.625)
+
+    def step(self, events=None):
+        """Append the token at position L0 everywhere, attend every layer,
+        rewind to L0."""
+        E, c = self.E, self.cfg
+        rc = E.lib().eakv_append_batch_device(self.handles, c["nseq"], self.tok.ptr, 1, None)
+        assert rc == 0, E.last_error()
+        for cache in self.caches:
+            cache.advance(1)
+        for l in range(c["nl"]):
+            if events:
+                events[l][0].record(self.stream)
+            rc = E.lib().eakv_attention_fused_batch_device(
+                self.handles, c["nseq"], l, self.ql[l].ptr, c["nq"], c["nkv"],
+                self.out.ptr, None)
+            assert rc == 0, E.last_error()
+            if events:
+                events[l][1].record(self.stream)
+        for cache in self.caches:
+            cache.restore(self.L0)
+
+    def prepare_step_inputs(self):
+        """New-token K/V in the batched-append layout
+        [seq][layer][kv][head][1][d] and per-layer queries [seq][q][d]."""
+        H, c = self.H, self.cfg
+        # one call per (seq, layer, kv) keeps row ids and channel scales aligned
+        for s in range(c["nseq"]):
+            for l in range(c["nl"]):
+                for kv, kind in ((0, c["k"]), (1, c["v"])):
+                    r0 = self.row0(s, l, kv)
+                    self.synth.fill(self.tok.ptr + r0 * c["d"] * 4, c["nkv"], 1, c["d"],
+                                    self.seed, r0, self.L0, kind,
+                                    self.chan.ptr + r0 * c["d"] * 4, self.stream)
+        self.ql = []
+        for l in range(c["nl"]):
+            a = H.DeviceArray((c["nseq"], c["nq"], c["d"]))
+            self.synth.fill(a.ptr, c["nseq"] * c["nq"], 1, c["d"], self.seed + 7,
+                            (l + 1) << 20, 0, "normal", stream=self.stream)
+            self.ql.append(a)
+
+    def fused_bytes(self):
+        c = self.cfg
+        ctx = self.L0 + 1
+        per_token_head = 2 * (c["d"] // 64) * 40
+        return c["nseq"] * (c["nkv"] * ctx * per_token_head + c["nq"] * c["d"] * 4 * 2)
+
+
+def cpu_baseline(cfg, budget_s=12.0):
+    """Time the oracle's two-pass fused attention (one sequence, one layer,
+    all q heads, full context) single-threaded and on up to 16 threads."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    nkv, nq, d, L = cfg["nkv"], cfg["nq"], cfg["d"], cfg["L"]
+    rng = np.random.default_rng(SEED_BASE)
+    oc = O.OracleCache(1, nkv, d, L)
+    data = rng.standard_normal((1, 2, nkv, L, d), dtype=np.float32)
+    oc.load_raw(data, L)
+    del data
+    q = rng.standard_normal((nq, d), dtype=np.float32)
+    t0 = time.perf_counter()
+    oc.attention_fused(q, 0, nq, nkv)
+    single = time.perf_counter() - t0
+    threads = max(1, min(16, os.cpu_count() or 1))
+    reps = max(1, int(budget_s / max(single, 1e-3) / 2))
+    reps = min(reps, 4 * threads)
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(lambda _: oc.attention_fused(q, 0, nq, nkv), range(reps)))
+    allcore = (time.perf_counter() - t0) / reps            # s per (seq, layer) unit
+    per_layer_us = lambda unit_s: unit_s * cfg["nseq"] * 1e6
+    return {
+        "value": round(per_layer_us(allcore), 1), "unit": "us/layer",
+        "cores": threads, "kind": "port",
+        "single_core_us_per_layer": round(per_layer_us(single), 1),
+        "sample": (f"oracle two-pass fused attention (C restatement of "
+                   f"fused_attention.ea, extended to GQA), 1 sequence x 1 layer, "
+                   f"{nq}q/{nkv}kv d{d} ctx {L}: 1 run single-threaded, {reps} runs on "
+                   f"{threads} threads; scaled x{cfg['nseq']} sequences per layer"),
+    }
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
+    ap.add_argument("--ctx", type=int, default=None, help="override context length")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
+              "sharding across GPUs is not built in this version", file=sys.stderr)
+        sys.exit(2)
+
+    from eakv_amd import hipmem as H
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)
+    w = Workload(args.config, args.ctx)
+    c = w.cfg
+    log(f"bench: config {args.config} {c['name']} ctx {w.L0 + 1}: filling caches")
+    w.fill_context()
+    w.prepare_step_inputs()
+    H.synchronize()
+    log(f"bench: quantize {w.quant_bytes / 1e9:.2f} GB alg in {w.quant_ms:.2f} ms "
+        f"({w.quant_bytes / w.quant_ms / 1e6:.0f} GB/s)")
+
+    for _ in range(args.warmup):
+        w.step()
+    H.synchronize()
+    events = [[H.Event(), H.Event()] for _ in range(c["nl"])]
+    fused_ms = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        w.step(events)
+        events[-1][1].synchronize()
+        fused_ms.append([e0.elapsed_ms(e1) for e0, e1 in events])
+    H.synchronize()
+    total_s = time.perf_counter() - t0
+    fused = np.array(fused_ms)
+    fused_us = float(fused.mean() * 1e3)
+    alg = w.fused_bytes()
+    achieved = alg / (fused_us * 1e-6) / 1e9
+    ms_step = total_s / args.steps * 1e3
+    log(f"bench: {ms_step:.3f} ms/step, fused {fused_us:.2f} us/layer "
+        f"(min {fused.min() * 1e3:.2f}), {achieved:.0f} GB/s")
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"fused_config{args.config}_traffic.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        log("bench: CPU baseline")
+        cpu = cpu_baseline(c)
+        cpu["cpu_model"] = cpu_model()
+
+    line = {
+        "metric": "fused Q4 attn µs/layer + achieved HBM GB/s, 32Q/8KV d128 32K ctx, 1 GPU",
+        "value": round(ms_step * 1e3 / c["nl"], 3),
+        "unit": "us/layer",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_1 (u8 nibbles + f32 scale/bias), f32 math",
+        "data": "synthetic: seeded device generator, distributions of the configuration",
+        "config": {"workload": c["name"], "layers": c["nl"], "q_heads": c["nq"],
+                   "kv_heads": c["nkv"], "head_dim": c["d"], "context": w.L0 + 1,
+                   "sequences": c["nseq"],
+                   "step": "append 1 token x all layers (K,V) + fused attention x all layers"},
+        "fused_us_per_layer": round(fused_us, 3),
+        "achieved_gbs": round(achieved, 1),
+        "quantize_gbs": round(w.quant_bytes / w.quant_ms / 1e6, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "alg_bytes_per_launch": alg},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

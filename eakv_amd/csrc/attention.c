@@ -1,0 +1,236 @@
+/* attention.c — attention dispatch (host C11).
+ *
+ * Reference src/attention.c:3-63 picks one of four CPU kernels from
+ * head_dim (64 or not) and n_q == n_kv.  Here the head_dim / GQA choice is
+ * made inside the HIP launchers (eakvd.h); this file validates, stages host
+ * buffers through the cache's device workspace and waits for the result.
+ */
+#include <string.h>
+
+#include "internal.h"
+
+static int attn_check(const eakv_cache_t *c, int layer, int n_q, int n_kv)
+{
+    if (!c) return eakvi_set_error(EAKV_ERR_INVALID, "attention: NULL cache");
+    if (c->head_dim != 64 && c->head_dim != 128)
+        return eakvi_set_error(EAKV_ERR_INVALID,
+                              "attention: head_dim %d not 64 or 128",
+                              c->head_dim);
+    if (layer < 0 || layer >= c->n_layers)
+        return eakvi_set_error(EAKV_ERR_INVALID, "attention: layer out of range");
+    if (n_kv <= 0 || n_kv > c->n_kv_heads || n_q < n_kv || n_q % n_kv != 0)
+        return eakvi_set_error(EAKV_ERR_INVALID,
+                              "attention: n_q %d / n_kv %d invalid for a cache "
+                              "of %d kv heads", n_q, n_kv, c->n_kv_heads);
+    return EAKV_OK;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+/* ------------------------------------------------------------------------ */
+/* K-score                                                                   */
+
+int eakv_attention_scores_device(const eakv_cache_t *c, const float *d_q,
+                                 int layer, int n_q, int n_kv,
+                                 float *d_scores, void *stream)
+{
+    int rc = attn_check(c, layer, n_q, n_kv);
+    if (rc) return rc;
+    if (!d_q || !d_scores)
+        return eakvi_set_error(EAKV_ERR_INVALID, "scores: NULL buffer");
+    int prev;
+    rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    int e = eakvd_k_score(&c->geom, c->dev, layer, c->seq_len, d_q, n_q, n_kv,
+                          d_scores, eakvi_stream_or_default(c, stream));
+    if (e) rc = eakvi_hip_fail(e, "k_score launch");
+    eakvi_leave(prev);
+    return rc;
+}
+
+/* reference src/attention.c:3-32 */
+void eakv_attention_scores(const eakv_cache_t *cc, const float *queries,
+                           int layer, int n_q, int n_kv, float *scores_out)
+{
+    eakv_cache_t *c = (eakv_cache_t *)cc;
+    if (attn_check(c, layer, n_q, n_kv)) return;
+    if (!queries || !scores_out) {
+        eakvi_set_error(EAKV_ERR_INVALID, "scores: NULL buffer");
+        return;
+    }
+    int prev;
+    if (eakvi_enter(c, &prev)) return;
+    const size_t qb = (size_t)n_q * c->head_dim * 4;
+    const size_t sb = (size_t)n_q * c->seq_len * 4;
+    int rc = eakvi_work_reserve(c, align256(qb) + sb);
+    if (rc == EAKV_OK) {
+        float *dq = (float *)c->work;
+        float *ds = (float *)((char *)c->work + align256(qb));
+        int e = eakvd_memcpy_h2d_async(dq, queries, qb, c->stream);
+        if (!e) e = eakvd_k_score(&c->geom, c->dev, layer, c->seq_len, dq, n_q,
+                                  n_kv, ds, c->stream);
+        if (!e && sb) e = eakvd_memcpy_d2h_async(scores_out, ds, sb, c->stream);
+        if (!e) e = eakvd_stream_sync(c->stream);
+        if (e) eakvi_hip_fail(e, "attention_scores");
+    }
+    eakvi_leave(prev);
+}
+
+/* ------------------------------------------------------------------------ */
+/* V-sum                                                                     */
+
+int eakv_attention_output_device(const eakv_cache_t *cc, const float *d_w,
+                                 int layer, int n_q, int n_kv, float *d_out,
+                                 void *stream)
+{
+    eakv_cache_t *c = (eakv_cache_t *)cc;
+    int rc = attn_check(c, layer, n_q, n_kv);
+    if (rc) return rc;
+    if (!d_w || !d_out)
+        return eakvi_set_error(EAKV_ERR_INVALID, "output: NULL buffer");
+    int prev;
+    rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    void *st = eakvi_stream_or_default(c, stream);
+    if (st != c->stream) {
+        /* the workspace is ordered on the cache's stream */
+        int e = eakvd_stream_sync(c->stream);
+        if (e) rc = eakvi_hip_fail(e, "output");
+    }
+    if (rc == EAKV_OK)
+        rc = eakvi_work_reserve(c, eakvd_v_sum_work_bytes(&c->geom, c->seq_len, n_q));
+    if (rc == EAKV_OK) {
+        int e = eakvd_v_sum(&c->geom, c->dev, layer, c->seq_len, d_w, n_q, n_kv,
+                            d_out, c->work, st);
+        if (e) rc = eakvi_hip_fail(e, "v_sum launch");
+    }
+    eakvi_leave(prev);
+    return rc;
+}
+
+/* reference src/attention.c:34-63 */
+void eakv_attention_output(const eakv_cache_t *cc, const float *weights,
+                           int layer, int n_q, int n_kv, float *output_out)
+{
+    eakv_cache_t *c = (eakv_cache_t *)cc;
+    if (attn_check(c, layer, n_q, n_kv)) return;
+    if (!weights || !output_out) {
+        eakvi_set_error(EAKV_ERR_INVALID, "output: NULL buffer");
+        return;
+    }
+    int prev;
+    if (eakvi_enter(c, &prev)) return;
+    const size_t wb = (size_t)n_q * c->seq_len * 4;
+    const size_t ob = (size_t)n_q * c->head_dim * 4;
+    const size_t pb = eakvd_v_sum_work_bytes(&c->geom, c->seq_len, n_q);
+    int rc = eakvi_work_reserve(c, align256(wb) + align256(ob) + pb);
+    if (rc == EAKV_OK) {
+        float *dw = (float *)c->work;
+        float *dout = (float *)((char *)c->work + align256(wb));
+        void *part = (char *)c->work + align256(wb) + align256(ob);
+        int e = wb ? eakvd_memcpy_h2d_async(dw, weights, wb, c->stream) : 0;
+        if (!e) e = eakvd_v_sum(&c->geom, c->dev, layer, c->seq_len, dw, n_q,
+                                n_kv, dout, part, c->stream);
+        if (!e) e = eakvd_memcpy_d2h_async(output_out, dout, ob, c->stream);
+        if (!e) e = eakvd_stream_sync(c->stream);
+        if (e) eakvi_hip_fail(e, "attention_output");
+    }
+    eakvi_leave(prev);
+}
+
+/* ------------------------------------------------------------------------ */
+/* fused decode attention                                                    */
+
+/* Partials go at the end of caches[0]'s workspace (reserved by the caller). */
+static int fused_launch(eakv_cache_t *const *caches, int n, int layer,
+                        const float *d_q, int n_q, int n_kv, float *d_out,
+                        void *stream)
+{
+    eakv_cache_t *c0 = caches[0];
+    eakvd_batch b;
+    memset(&b, 0, sizeof(b));
+    b.n_seq = n;
+    for (int i = 0; i < n; i++) {
+        b.base[i] = caches[i]->dev;
+        b.seq_len[i] = caches[i]->seq_len;
+    }
+    const size_t need = eakvd_fused_work_bytes(&c0->geom, &b, n_q);
+    return eakvd_fused(&c0->geom, &b, layer, d_q, n_q, n_kv, d_out,
+                       (char *)c0->work + (c0->work_bytes - need), stream);
+}
+
+int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
+                                      int n_caches, int layer,
+                                      const float *d_q, int n_q, int n_kv,
+                                      float *d_out, void *stream)
+{
+    if (!caches || n_caches <= 0 || n_caches > EAKVD_MAX_BATCH || !d_q || !d_out)
+        return eakvi_set_error(EAKV_ERR_INVALID, "fused_batch: invalid argument");
+    for (int i = 0; i < n_caches; i++) {
+        if (!caches[i])
+            return eakvi_set_error(EAKV_ERR_INVALID, "fused_batch: NULL cache");
+        const eakv_cache_t *a = caches[0], *b = caches[i];
+        if (a->n_layers != b->n_layers || a->n_kv_heads != b->n_kv_heads ||
+            a->head_dim != b->head_dim || a->max_seq_len != b->max_seq_len ||
+            a->device != b->device)
+            return eakvi_set_error(EAKV_ERR_INVALID,
+                                  "fused_batch: caches differ in shape");
+    }
+    eakv_cache_t *c0 = caches[0];
+    int rc = attn_check(c0, layer, n_q, n_kv);
+    if (rc) return rc;
+    int prev;
+    rc = eakvi_enter(c0, &prev);
+    if (rc) return rc;
+    void *st = eakvi_stream_or_default(c0, stream);
+    if (st != c0->stream) {
+        int e = eakvd_stream_sync(c0->stream);
+        if (e) rc = eakvi_hip_fail(e, "fused_batch");
+    }
+    eakvd_batch b;
+    memset(&b, 0, sizeof(b));
+    b.n_seq = n_caches;
+    for (int i = 0; i < n_caches; i++) b.seq_len[i] = caches[i]->seq_len;
+    if (rc == EAKV_OK)
+        rc = eakvi_work_reserve(c0, eakvd_fused_work_bytes(&c0->geom, &b, n_q));
+    if (rc == EAKV_OK) {
+        int e = fused_launch(caches, n_caches, layer, d_q, n_q, n_kv, d_out, st);
+        if (e) rc = eakvi_hip_fail(e, "fused launch");
+    }
+    eakvi_leave(prev);
+    return rc;
+}
+
+int eakv_attention_fused(const eakv_cache_t *cc, const float *queries,
+                         int layer, int n_q, int n_kv, float *output_out)
+{
+    eakv_cache_t *c = (eakv_cache_t *)cc;
+    int rc = attn_check(c, layer, n_q, n_kv);
+    if (rc) return rc;
+    if (!queries || !output_out)
+        return eakvi_set_error(EAKV_ERR_INVALID, "fused: NULL buffer");
+    int prev;
+    rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    eakvd_batch b;
+    memset(&b, 0, sizeof(b));
+    b.n_seq = 1;
+    b.seq_len[0] = c->seq_len;
+    const size_t io = align256((size_t)n_q * c->head_dim * 4);
+    const size_t pb = eakvd_fused_work_bytes(&c->geom, &b, n_q);
+    rc = eakvi_work_reserve(c, 2 * io + pb);
+    if (rc == EAKV_OK) {
+        float *dq = (float *)c->work;
+        float *dout = (float *)((char *)c->work + io);
+        int e = eakvd_memcpy_h2d_async(dq, queries,
+                                       (size_t)n_q * c->head_dim * 4, c->stream);
+        if (!e) e = fused_launch(&c, 1, layer, dq, n_q, n_kv, dout, c->stream);
+        if (!e) e = eakvd_memcpy_d2h_async(output_out, dout,
+                                           (size_t)n_q * c->head_dim * 4,
+                                           c->stream);
+        if (!e) e = eakvd_stream_sync(c->stream);
+        if (e) rc = eakvi_hip_fail(e, "attention_fused");
+    }
+    eakvi_leave(prev);
+    return rc;
+}

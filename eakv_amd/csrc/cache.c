@@ -1,0 +1,417 @@
+/* cache.c — cache lifecycle and quantization drivers (host C11).
+ *
+ * Follows reference src/cache.c:5-201: validation, error codes and seq_len
+ * semantics are the reference's; the planes live in device memory and the
+ * per-(layer, kv, head) quantize loop of the reference (cache.c:76-95,
+ * :135-147) becomes one kernel launch over all groups.
+ */
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "internal.h"
+
+/* ------------------------------------------------------------------------ */
+/* error side channel                                                        */
+
+static _Thread_local int  tl_err;
+static _Thread_local char tl_msg[256];
+
+int eakvi_set_error(int code, const char *fmt, ...)
+{
+    va_list ap;
+    tl_err = code;
+    va_start(ap, fmt);
+    vsnprintf(tl_msg, sizeof(tl_msg), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int eakvi_hip_fail(int hip_err, const char *what)
+{
+    /* hipErrorOutOfMemory == 2 */
+    int code = hip_err == 2 ? EAKV_ERR_ALLOC : EAKV_ERR_DEVICE;
+    return eakvi_set_error(code, "%s: %s", what, eakvd_error_string(hip_err));
+}
+
+int eakv_last_error(void) { return tl_err; }
+const char *eakv_last_error_message(void) { return tl_err ? tl_msg : ""; }
+void eakv_clear_error(void) { tl_err = 0; tl_msg[0] = 0; }
+
+/* ------------------------------------------------------------------------ */
+/* layout and device helpers                                                 */
+
+static int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+void eakvd_geom_init(eakvd_geom *g, int n_layers, int n_kv_heads,
+                     int head_dim, int max_seq_len)
+{
+    g->n_layers = n_layers;
+    g->n_kv_heads = n_kv_heads;
+    g->head_dim = head_dim;
+    g->max_seq_len = max_seq_len;
+    g->gpd = head_dim / 64;
+    g->gph = (int64_t)max_seq_len * g->gpd;
+    /* groups_per_token * max_seq_len (reference src/cache.c:26-27) */
+    g->max_groups = (int64_t)n_kv_heads * head_dim / 64 * max_seq_len;
+    g->s_off = round256(g->max_groups * 32);
+    g->b_off = g->s_off + round256(g->max_groups * 4);
+    g->block_bytes = g->b_off + round256(g->max_groups * 4);
+}
+
+int eakvi_enter(const eakv_cache_t *c, int *prev)
+{
+    int e = eakvd_get_device(prev);
+    if (e) return eakvi_hip_fail(e, "hipGetDevice");
+    if (*prev != c->device) {
+        e = eakvd_set_device(c->device);
+        if (e) return eakvi_hip_fail(e, "hipSetDevice");
+    }
+    return EAKV_OK;
+}
+
+void eakvi_leave(int prev)
+{
+    int cur = -1;
+    if (eakvd_get_device(&cur) == 0 && cur != prev) eakvd_set_device(prev);
+}
+
+int eakvi_work_reserve(eakv_cache_t *c, size_t n)
+{
+    if (n <= c->work_bytes) return EAKV_OK;
+    int e = eakvd_stream_sync(c->stream);
+    if (e) return eakvi_hip_fail(e, "stream sync");
+    if (c->work) eakvd_free(c->work);
+    c->work = NULL;
+    c->work_bytes = 0;
+    size_t want = n + n / 4;
+    e = eakvd_malloc(&c->work, want);
+    if (e) {
+        c->work = NULL;
+        return eakvi_hip_fail(e, "workspace hipMalloc");
+    }
+    c->work_bytes = want;
+    return EAKV_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* lifecycle: reference src/cache.c:11-58                                    */
+
+eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
+                                int max_seq_len)
+{
+    if (n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 ||
+        max_seq_len <= 0) {
+        eakvi_set_error(EAKV_ERR_INVALID, "cache_create: non-positive dimension");
+        return NULL;
+    }
+    if (((int64_t)n_kv_heads * head_dim) % 64 != 0) {
+        eakvi_set_error(EAKV_ERR_INVALID,
+                       "cache_create: n_kv_heads*head_dim not a multiple of 64");
+        return NULL;
+    }
+    eakv_cache_t *c = calloc(1, sizeof(*c));
+    if (!c) {
+        eakvi_set_error(EAKV_ERR_ALLOC, "cache_create: out of host memory");
+        return NULL;
+    }
+    c->n_layers = n_layers;
+    c->n_kv_heads = n_kv_heads;
+    c->head_dim = head_dim;
+    c->max_seq_len = max_seq_len;
+    eakvd_geom_init(&c->geom, n_layers, n_kv_heads, head_dim, max_seq_len);
+    c->dev_bytes = (size_t)c->geom.block_bytes * 2 * (size_t)n_layers;
+
+    int e = eakvd_get_device(&c->device);
+    if (e) goto hip_fail;
+    e = eakvd_stream_create(&c->stream);
+    if (e) goto hip_fail;
+    e = eakvd_malloc((void **)&c->dev, c->dev_bytes);
+    if (e) goto hip_fail;
+    /* the reference calloc()s its planes (cache.c:33) */
+    e = eakvd_memset_async(c->dev, 0, c->dev_bytes, c->stream);
+    if (!e) e = eakvd_stream_sync(c->stream);
+    if (e) goto hip_fail;
+    return c;
+
+hip_fail:
+    eakvi_hip_fail(e, "cache_create");
+    if (c->dev) eakvd_free(c->dev);
+    if (c->stream) eakvd_stream_destroy(c->stream);
+    free(c);
+    return NULL;
+}
+
+void eakv_cache_free(eakv_cache_t *c)
+{
+    if (!c) return;
+    int prev;
+    int ok = eakvi_enter(c, &prev) == EAKV_OK;
+    if (c->stream) eakvd_stream_sync(c->stream);
+    if (c->work) eakvd_free(c->work);
+    if (c->dev) eakvd_free(c->dev);
+    if (c->stream) eakvd_stream_destroy(c->stream);
+    if (ok) eakvi_leave(prev);
+    free(c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* quantization drivers                                                      */
+
+/* Quantize rows of `src` (device) into cache c: rows are (plane, head) for
+ * planes plane0..plane0+n_planes-1, each n_g groups, row stride row_stride
+ * floats, written at token offset t_off. */
+static int quant_rows(eakv_cache_t *c, const float *src, int64_t row_stride,
+                      int plane0, int n_planes, int64_t n_tok, int t_off,
+                      void *stream)
+{
+    eakvd_quant_job job;
+    memset(&job, 0, sizeof(job));
+    job.src = src;
+    job.row_stride = row_stride;
+    job.n_rows = (int64_t)n_planes * c->n_kv_heads;
+    job.n_g = n_tok * c->geom.gpd;
+    job.nh = c->n_kv_heads;
+    job.n_planes = n_planes;
+    job.plane0 = plane0;
+    job.n_caches = 1;
+    job.base[0] = c->dev;
+    job.g_off[0] = (int64_t)t_off * c->geom.gpd;
+    int e = eakvd_quantize(&c->geom, &job, stream);
+    return e ? eakvi_hip_fail(e, "quantize launch") : EAKV_OK;
+}
+
+/* reference src/cache.c:60-100 */
+int eakv_cache_load_raw(eakv_cache_t *c, const float *data, int seq_len)
+{
+    if (!c || !data || seq_len <= 0)
+        return eakvi_set_error(EAKV_ERR_INVALID, "load_raw: invalid argument");
+    if (seq_len > c->max_seq_len)
+        return eakvi_set_error(EAKV_ERR_INVALID, "load_raw: seq_len > max_seq_len");
+    int prev, rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+
+    /* Stage whole (layer, kv) planes through the device workspace, at most
+     * ~256 MB (but at least one plane) per copy. */
+    const int64_t row_elems = (int64_t)seq_len * c->head_dim;
+    const int64_t plane_bytes = row_elems * c->n_kv_heads * 4;
+    const int n_planes = 2 * c->n_layers;
+    int per = (int)((256ll << 20) / (plane_bytes ? plane_bytes : 1));
+    if (per < 1) per = 1;
+    if (per > n_planes) per = n_planes;
+    rc = eakvi_work_reserve(c, (size_t)plane_bytes * per);
+    for (int p0 = 0; rc == EAKV_OK && p0 < n_planes; p0 += per) {
+        int np = n_planes - p0 < per ? n_planes - p0 : per;
+        int e = eakvd_memcpy_h2d_async(c->work, data + (int64_t)p0 * row_elems *
+                                                            c->n_kv_heads,
+                                       (size_t)plane_bytes * np, c->stream);
+        if (e) { rc = eakvi_hip_fail(e, "load_raw H2D"); break; }
+        rc = quant_rows(c, (const float *)c->work, row_elems, p0, np, seq_len,
+                        0, c->stream);
+    }
+    if (rc == EAKV_OK) {
+        int e = eakvd_stream_sync(c->stream);
+        if (e) rc = eakvi_hip_fail(e, "load_raw");
+    }
+    if (rc == EAKV_OK) c->seq_len = seq_len;
+    eakvi_leave(prev);
+    return rc;
+}
+
+int eakv_cache_load_raw_device(eakv_cache_t *c, const float *d_data,
+                               int seq_len, void *stream)
+{
+    if (!c || !d_data || seq_len <= 0)
+        return eakvi_set_error(EAKV_ERR_INVALID, "load_raw: invalid argument");
+    if (seq_len > c->max_seq_len)
+        return eakvi_set_error(EAKV_ERR_INVALID, "load_raw: seq_len > max_seq_len");
+    int prev, rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    rc = quant_rows(c, d_data, (int64_t)seq_len * c->head_dim, 0,
+                    2 * c->n_layers, seq_len, 0,
+                    eakvi_stream_or_default(c, stream));
+    if (rc == EAKV_OK) c->seq_len = seq_len;
+    eakvi_leave(prev);
+    return rc;
+}
+
+static int append_check(const eakv_cache_t *c, const void *data, int layer,
+                        int kv_idx, int n_tokens)
+{
+    if (!c || !data || n_tokens <= 0)
+        return eakvi_set_error(EAKV_ERR_INVALID, "append: invalid argument");
+    if (layer < 0 || layer >= c->n_layers)
+        return eakvi_set_error(EAKV_ERR_INVALID, "append: layer out of range");
+    if (kv_idx < 0 || kv_idx > 1)
+        return eakvi_set_error(EAKV_ERR_INVALID, "append: kv_idx not 0 or 1");
+    if ((int64_t)c->seq_len + n_tokens > c->max_seq_len)
+        return eakvi_set_error(EAKV_ERR_INVALID, "append: exceeds max_seq_len");
+    return EAKV_OK;
+}
+
+/* reference src/cache.c:102-151 */
+int eakv_cache_append(eakv_cache_t *c, const float *data, int layer,
+                      int kv_idx, int n_tokens)
+{
+    int rc = append_check(c, data, layer, kv_idx, n_tokens);
+    if (rc) return rc;
+    int prev;
+    rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    const int64_t row_elems = (int64_t)n_tokens * c->head_dim;
+    const size_t bytes = (size_t)row_elems * c->n_kv_heads * 4;
+    rc = eakvi_work_reserve(c, bytes);
+    if (rc == EAKV_OK) {
+        int e = eakvd_memcpy_h2d_async(c->work, data, bytes, c->stream);
+        if (e) rc = eakvi_hip_fail(e, "append H2D");
+    }
+    if (rc == EAKV_OK)
+        rc = quant_rows(c, (const float *)c->work, row_elems,
+                        layer * 2 + kv_idx, 1, n_tokens, c->seq_len, c->stream);
+    if (rc == EAKV_OK) {
+        int e = eakvd_stream_sync(c->stream);
+        if (e) rc = eakvi_hip_fail(e, "append");
+    }
+    eakvi_leave(prev);
+    return rc;
+}
+
+int eakv_cache_append_device(eakv_cache_t *c, const float *d_data, int layer,
+                             int kv_idx, int n_tokens, void *stream)
+{
+    int rc = append_check(c, d_data, layer, kv_idx, n_tokens);
+    if (rc) return rc;
+    int prev;
+    rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    rc = quant_rows(c, d_data, (int64_t)n_tokens * c->head_dim,
+                    layer * 2 + kv_idx, 1, n_tokens, c->seq_len,
+                    eakvi_stream_or_default(c, stream));
+    eakvi_leave(prev);
+    return rc;
+}
+
+static int same_shape(const eakv_cache_t *a, const eakv_cache_t *b)
+{
+    return a->n_layers == b->n_layers && a->n_kv_heads == b->n_kv_heads &&
+           a->head_dim == b->head_dim && a->max_seq_len == b->max_seq_len &&
+           a->device == b->device;
+}
+
+int eakv_append_batch_device(eakv_cache_t *const *caches, int n_caches,
+                             const float *d_data, int n_tokens, void *stream)
+{
+    if (!caches || n_caches <= 0 || n_caches > EAKVD_MAX_BATCH || !d_data ||
+        n_tokens <= 0)
+        return eakvi_set_error(EAKV_ERR_INVALID, "append_batch: invalid argument");
+    for (int i = 0; i < n_caches; i++) {
+        if (!caches[i] || !same_shape(caches[0], caches[i]))
+            return eakvi_set_error(EAKV_ERR_INVALID,
+                                  "append_batch: caches differ in shape");
+        if ((int64_t)caches[i]->seq_len + n_tokens > caches[i]->max_seq_len)
+            return eakvi_set_error(EAKV_ERR_INVALID,
+                                  "append_batch: exceeds max_seq_len");
+    }
+    eakv_cache_t *c0 = caches[0];
+    int prev, rc = eakvi_enter(c0, &prev);
+    if (rc) return rc;
+    eakvd_quant_job job;
+    memset(&job, 0, sizeof(job));
+    job.src = d_data;
+    job.row_stride = (int64_t)n_tokens * c0->head_dim;
+    job.n_rows = (int64_t)n_caches * 2 * c0->n_layers * c0->n_kv_heads;
+    job.n_g = (int64_t)n_tokens * c0->geom.gpd;
+    job.nh = c0->n_kv_heads;
+    job.n_planes = 2 * c0->n_layers;
+    job.plane0 = 0;
+    job.n_caches = n_caches;
+    for (int i = 0; i < n_caches; i++) {
+        job.base[i] = caches[i]->dev;
+        job.g_off[i] = (int64_t)caches[i]->seq_len * c0->geom.gpd;
+    }
+    int e = eakvd_quantize(&c0->geom, &job, eakvi_stream_or_default(c0, stream));
+    if (e) rc = eakvi_hip_fail(e, "append_batch launch");
+    eakvi_leave(prev);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* seq_len bookkeeping: reference src/cache.c:153-201                        */
+
+int eakv_cache_advance(eakv_cache_t *c, int n_tokens)
+{
+    if (!c || n_tokens <= 0)
+        return eakvi_set_error(EAKV_ERR_INVALID, "advance: invalid argument");
+    if ((int64_t)c->seq_len + n_tokens > c->max_seq_len)
+        return eakvi_set_error(EAKV_ERR_INVALID, "advance: exceeds max_seq_len");
+    c->seq_len += n_tokens;
+    return EAKV_OK;
+}
+
+void eakv_cache_clear(eakv_cache_t *c)
+{
+    if (c) c->seq_len = 0;
+}
+
+int eakv_checkpoint(eakv_cache_t *c) { return c ? c->seq_len : 0; }
+
+int eakv_restore(eakv_cache_t *c, int seq_len)
+{
+    if (!c) return eakvi_set_error(EAKV_ERR_INVALID, "restore: NULL cache");
+    if (seq_len < 0 || seq_len > c->seq_len)
+        return eakvi_set_error(EAKV_ERR_INVALID, "restore: seq_len out of range");
+    c->seq_len = seq_len;
+    return EAKV_OK;
+}
+
+int eakv_cache_seq_len(const eakv_cache_t *c) { return c ? c->seq_len : 0; }
+int eakv_cache_n_layers(const eakv_cache_t *c) { return c ? c->n_layers : 0; }
+int eakv_cache_n_heads(const eakv_cache_t *c) { return c ? c->n_kv_heads : 0; }
+int eakv_cache_head_dim(const eakv_cache_t *c) { return c ? c->head_dim : 0; }
+int eakv_cache_max_seq_len(const eakv_cache_t *c)
+{
+    return c ? c->max_seq_len : 0;
+}
+
+float eakv_cache_compression_ratio(const eakv_cache_t *c)
+{
+    if (!c || c->seq_len == 0) return 0.0f;
+    return 40.0f / 256.0f;
+}
+
+int eakv_cache_device(const eakv_cache_t *c) { return c ? c->device : -1; }
+void *eakv_cache_stream(const eakv_cache_t *c) { return c ? c->stream : NULL; }
+
+int eakv_cache_sync(const eakv_cache_t *c)
+{
+    if (!c) return eakvi_set_error(EAKV_ERR_INVALID, "sync: NULL cache");
+    int prev, rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    int e = eakvd_stream_sync(c->stream);
+    if (e) rc = eakvi_hip_fail(e, "sync");
+    eakvi_leave(prev);
+    return rc;
+}
+
+int eakv_cache_read_planes(const eakv_cache_t *c, int layer, int kv_idx,
+                           uint8_t *weights, float *scales, float *biases)
+{
+    if (!c || layer < 0 || layer >= c->n_layers || kv_idx < 0 || kv_idx > 1)
+        return eakvi_set_error(EAKV_ERR_INVALID, "read_planes: invalid argument");
+    int prev, rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    const uint8_t *blk =
+        c->dev + (int64_t)(layer * 2 + kv_idx) * c->geom.block_bytes;
+    const size_t ng = (size_t)c->geom.max_groups;
+    int e = 0;
+    if (weights) e = eakvd_memcpy_d2h_async(weights, blk, ng * 32, c->stream);
+    if (!e && scales)
+        e = eakvd_memcpy_d2h_async(scales, blk + c->geom.s_off, ng * 4, c->stream);
+    if (!e && biases)
+        e = eakvd_memcpy_d2h_async(biases, blk + c->geom.b_off, ng * 4, c->stream);
+    if (!e) e = eakvd_stream_sync(c->stream);
+    if (e) rc = eakvi_hip_fail(e, "read_planes");
+    eakvi_leave(prev);
+    return rc;
+}

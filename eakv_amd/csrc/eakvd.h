@@ -1,0 +1,109 @@
+/* eakvd.h — the thin C ABI between the C11 host library and the gfx950 HIP
+ * kernels.  Plain C: no HIP types cross this boundary (streams are void*).
+ *
+ * Device layout of one cache (one hipMalloc, zero-filled):
+ *   block p = layer*2 + kv  at  base + p*block_bytes, holding three planes
+ *     weights  u8 [max_groups*32]   at block + 0
+ *     scales   f32[max_groups]      at block + s_off
+ *     biases   f32[max_groups]      at block + b_off
+ *   group index inside a plane = h*gph + t*gpd + j  (gph = max_seq_len*gpd,
+ *   gpd = head_dim/64), the indexing of reference src/cache.c:69,:137 and
+ *   src/attention.c:7.  Block and plane starts are rounded up to 256 bytes.
+ */
+#ifndef EAKVD_H
+#define EAKVD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Sequences per batched launch (kernel-argument arrays). */
+#define EAKVD_MAX_BATCH 32
+
+typedef struct {
+    int     n_layers, n_kv_heads, head_dim, max_seq_len;
+    int64_t gpd;          /* groups per token per head */
+    int64_t gph;          /* groups per head in a plane */
+    int64_t max_groups;   /* groups per plane */
+    int64_t s_off, b_off; /* plane offsets inside a block, bytes */
+    int64_t block_bytes;  /* bytes per (layer, kv) block */
+} eakvd_geom;
+
+void eakvd_geom_init(eakvd_geom *g, int n_layers, int n_kv_heads,
+                     int head_dim, int max_seq_len);
+
+/* ---- runtime (hip/runtime.hip); every function returns 0 or a HIP error */
+int  eakvd_get_device(int *dev);
+int  eakvd_set_device(int dev);
+int  eakvd_malloc(void **p, size_t n);
+int  eakvd_free(void *p);
+int  eakvd_host_malloc(void **p, size_t n);   /* pinned */
+int  eakvd_host_free(void *p);
+int  eakvd_stream_create(void **s);
+int  eakvd_stream_destroy(void *s);
+int  eakvd_stream_sync(void *s);
+int  eakvd_memset_async(void *p, int v, size_t n, void *s);
+int  eakvd_memcpy_h2d_async(void *dst, const void *src, size_t n, void *s);
+int  eakvd_memcpy_d2h_async(void *dst, const void *src, size_t n, void *s);
+int  eakvd_memcpy_d2d_async(void *dst, const void *src, size_t n, void *s);
+const char *eakvd_error_string(int err);
+
+/* ---- quantize (hip/quantize.hip)
+ * Source row r starts at src + r*row_stride and holds n_g groups of 64
+ * contiguous f32.  Row r maps to cache c = r / (n_planes*nh),
+ * plane = plane0 + (r / nh) % n_planes, head h = r % nh, and writes groups
+ * h*gph + g_off[c] + g, g < n_g. */
+typedef struct {
+    const float *src;
+    int64_t      row_stride;
+    int64_t      n_rows;
+    int64_t      n_g;
+    int          nh;
+    int          n_planes;
+    int          plane0;
+    int          n_caches;
+    uint8_t     *base[EAKVD_MAX_BATCH];
+    int64_t      g_off[EAKVD_MAX_BATCH];
+} eakvd_quant_job;
+
+int eakvd_quantize(const eakvd_geom *g, const eakvd_quant_job *job,
+                   void *stream);
+
+/* ---- attention kernels (hip/kscore.hip, hip/vsum.hip, hip/fused.hip)
+ * Plane pointers come from one cache's device base and a layer. */
+
+/* scores[qh*seq_len + t], q: [n_q][head_dim] (device pointers) */
+int eakvd_k_score(const eakvd_geom *g, const uint8_t *base, int layer,
+                  int seq_len, const float *q, int n_q, int n_kv,
+                  float *scores, void *stream);
+
+/* out[qh*head_dim + i] = sum_t w[qh*seq_len + t] * dequant(V[kv][t][i]).
+ * work: device scratch of eakvd_v_sum_work_bytes() bytes. */
+size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len, int n_q);
+int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base, int layer,
+                int seq_len, const float *w, int n_q, int n_kv, float *out,
+                void *work, void *stream);
+
+/* Fused decode attention over a batch of same-geometry caches:
+ * out[s][qh][i] = softmax_t(q[s][qh].K[s][kv][t] / sqrt(d)) . V[s][kv][t][i]
+ * q, out: [n_seq][n_q][head_dim] device pointers. */
+typedef struct {
+    int            n_seq;
+    const uint8_t *base[EAKVD_MAX_BATCH];
+    int            seq_len[EAKVD_MAX_BATCH];
+} eakvd_batch;
+
+size_t eakvd_fused_work_bytes(const eakvd_geom *g, const eakvd_batch *b,
+                              int n_q);
+int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
+                const float *q, int n_q, int n_kv, float *out, void *work,
+                void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

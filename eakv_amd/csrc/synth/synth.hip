@@ -1,0 +1,77 @@
+// synth.hip — seeded synthetic KV / query generator on the device, for the
+// benchmark and the full-size tests (libeakv_synth.so; not part of the eakv
+// API).  Value (row, pos, dim) depends only on (seed, row, pos, dim), so any
+// slice of a cache — a whole layer, one appended token — can be regenerated
+// independently and identically.
+//
+//   v = N(0,1) * sigma * chan[row][dim] * (1 + drift_amp*sin(pos/drift_period))
+//   with probability outlier_p, v = +-outlier_v instead
+// N(0,1) by Box-Muller from a splitmix64 hash of the counter.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+extern "C" {
+typedef struct {
+    uint64_t     seed;
+    int64_t      row0;         // hash id of the first row
+    int64_t      pos0;         // position of the first token
+    float        sigma;
+    const float *chan;         // device [n_rows][d] or NULL
+    float        drift_amp, drift_period;
+    float        outlier_p, outlier_v;
+} eakv_synth_params;
+}
+
+namespace {
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void synth_kernel(float *__restrict__ out,
+                                                    int64_t n, int64_t n_tok,
+                                                    int d, eakv_synth_params p)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256) {
+        const int dim = (int)(i % d);
+        const int64_t rt = i / d;
+        const int64_t tok = rt % n_tok, r = rt / n_tok;
+        const int64_t pos = p.pos0 + tok;
+        const uint64_t ctr = ((uint64_t)(p.row0 + r) << 40) ^
+                             ((uint64_t)pos << 12) ^ (uint64_t)dim;
+        const uint64_t h = mix64(p.seed ^ mix64(ctr));
+        const float u1 = ((float)(h >> 40) + 1.0f) * (1.0f / 16777216.0f);
+        const float u2 = (float)((h >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+        float v = sqrtf(-2.0f * logf(u1)) * cosf(6.2831853071795865f * u2);
+        v *= p.sigma;
+        if (p.chan) v *= p.chan[r * d + dim];
+        if (p.drift_amp != 0.0f)
+            v *= 1.0f + p.drift_amp * sinf((float)pos / p.drift_period);
+        if (p.outlier_p > 0.0f) {
+            const uint64_t h2 = mix64(h ^ 0xD1B54A32D192ED03ull);
+            const float u3 = (float)(h2 >> 40) * (1.0f / 16777216.0f);
+            if (u3 < p.outlier_p) v = (h2 & 1) ? p.outlier_v : -p.outlier_v;
+        }
+        out[i] = v;
+    }
+}
+
+}  // namespace
+
+// out[r][t][i] for r < n_rows, t < n_tok, i < d.
+extern "C" int eakv_synth_fill(float *out, int64_t n_rows, int64_t n_tok, int d,
+                               const eakv_synth_params *p, void *stream)
+{
+    const int64_t n = n_rows * n_tok * d;
+    if (n <= 0) return 0;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(synth_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, out, n, n_tok, d, *p);
+    return (int)hipGetLastError();
+}

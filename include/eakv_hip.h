@@ -1,0 +1,91 @@
+/* eakv_hip.h — MI355X extensions to the eakv C API (include/eakv.h).
+ *
+ * None of these has a counterpart in the reference, whose caches live in host
+ * memory.  They exist because the reference API takes host pointers, which
+ * forces a PCIe round trip per call on a GPU:
+ *   - device-pointer forms of load/append/scores/output, asynchronous on a
+ *     HIP stream (pass the hipStream_t as void*, NULL = the cache's own);
+ *   - batched append and batched fused decode attention over several caches
+ *     of the same shape (one launch per layer for all sequences);
+ *   - the fused single-pass softmax attention, which the reference compiles
+ *     (kernels/fused_attention.ea:190-373) but never wires into its C API;
+ *   - plane read-back and an error side channel for the void attention calls.
+ * Device-pointer calls return when the work is enqueued; results are ready
+ * after eakv_cache_sync() or a wait on the stream.
+ */
+#ifndef EAKV_HIP_H
+#define EAKV_HIP_H
+
+#include <stdint.h>
+
+#include "eakv.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A HIP runtime or kernel launch failure. */
+#define EAKV_ERR_DEVICE     -5
+
+/* Most recent error recorded by a call on this thread (EAKV_OK if none since
+ * eakv_clear_error) and its message. */
+int         eakv_last_error(void);
+const char *eakv_last_error_message(void);
+void        eakv_clear_error(void);
+
+/* The HIP device ordinal the cache lives on, its stream, and a wait for all
+ * work enqueued on that stream. */
+int   eakv_cache_device(const eakv_cache_t *cache);
+void *eakv_cache_stream(const eakv_cache_t *cache);
+int   eakv_cache_sync(const eakv_cache_t *cache);
+
+/* Copy the planes of block (layer, kv_idx) to host buffers holding
+ * n_kv_heads*max_seq_len*head_dim/64 groups each (weights 32 B per group). */
+int eakv_cache_read_planes(const eakv_cache_t *cache, int layer, int kv_idx,
+                           uint8_t *weights, float *scales, float *biases);
+
+/* eakv_cache_load_raw / eakv_cache_append with device input (same layout and
+ * validation; seq_len is set by load_raw and untouched by append). */
+int eakv_cache_load_raw_device(eakv_cache_t *cache, const float *d_data,
+                               int seq_len, void *stream);
+int eakv_cache_append_device(eakv_cache_t *cache, const float *d_data,
+                             int layer, int kv_idx, int n_tokens,
+                             void *stream);
+
+/* Append n_tokens to every layer and both K/V of n_caches caches in one
+ * launch.  d_data: f32[n_caches][n_layers][2][n_kv_heads][n_tokens][head_dim].
+ * Caches must share n_layers, n_kv_heads, head_dim, max_seq_len and device;
+ * seq_len is not changed (call eakv_cache_advance on each). */
+int eakv_append_batch_device(eakv_cache_t *const *caches, int n_caches,
+                             const float *d_data, int n_tokens, void *stream);
+
+/* eakv_attention_scores / eakv_attention_output on device buffers. */
+int eakv_attention_scores_device(const eakv_cache_t *cache, const float *d_q,
+                                 int layer, int n_q_heads, int n_kv_heads,
+                                 float *d_scores, void *stream);
+int eakv_attention_output_device(const eakv_cache_t *cache,
+                                 const float *d_weights, int layer,
+                                 int n_q_heads, int n_kv_heads, float *d_out,
+                                 void *stream);
+
+/* Fused decode attention softmax(q.K^T/sqrt(d)).V over the cache's seq_len
+ * tokens, host pointers, synchronous: queries f32[n_q][head_dim],
+ * output_out f32[n_q][head_dim]. */
+int eakv_attention_fused(const eakv_cache_t *cache, const float *queries,
+                         int layer, int n_q_heads, int n_kv_heads,
+                         float *output_out);
+
+/* Fused decode attention for n_caches same-shape caches (each over its own
+ * seq_len) in one launch: d_q, d_out f32[n_caches][n_q][head_dim].  Uses the
+ * workspace of caches[0]; a call counts as a use of every cache it names. */
+int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
+                                      int n_caches, int layer,
+                                      const float *d_q, int n_q_heads,
+                                      int n_kv_heads, float *d_out,
+                                      void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EAKV_HIP_H */

@@ -1,0 +1,253 @@
+"""ctypes binding of the CPU oracle (liboracle.so) — TEST INFRASTRUCTURE ONLY.
+
+Loaded by tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg as
+the checker; never by the eakv_amd package.  ``OracleCache`` offers the same
+methods as ``eakv_amd.Cache`` so one test body can drive either.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_LIB_PATH = os.path.join(HERE, "_ref", "libggml_ref.so")
+
+_vp = C.c_void_p
+_i64 = C.c_int64
+
+_SIG = {
+    "orc_quantize_split": (None, [_vp, _vp, _vp, _vp, _i64]),
+    "orc_reduce16": (C.c_float, [_vp]),
+    "orc_dequantize": (None, [_vp, _vp, _vp, _vp, _i64]),
+    "orc_to_i32": (C.c_int32, [C.c_float]),
+    "orc_k_score_mha": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _i64]),
+    "orc_k_score_gqa": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _i64]),
+    "orc_v_sum_mha": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _i64]),
+    "orc_v_sum_gqa": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _i64]),
+    "orc_fused_attention": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   C.c_int, C.c_int, C.c_int, _i64]),
+    "orc_softmax_rows": (None, [_vp, _vp, C.c_int, C.c_int]),
+    "orc_cache_create": (_vp, [C.c_int] * 4),
+    "orc_cache_free": (None, [_vp]),
+    "orc_cache_load_raw": (C.c_int, [_vp, _vp, C.c_int]),
+    "orc_cache_append": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "orc_cache_advance": (C.c_int, [_vp, C.c_int]),
+    "orc_cache_clear": (None, [_vp]),
+    "orc_checkpoint": (C.c_int, [_vp]),
+    "orc_restore": (C.c_int, [_vp, C.c_int]),
+    "orc_attention_scores": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "orc_attention_output": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "orc_attention_fused": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "orc_cache_seq_len": (C.c_int, [_vp]),
+    "orc_cache_n_layers": (C.c_int, [_vp]),
+    "orc_cache_n_heads": (C.c_int, [_vp]),
+    "orc_cache_head_dim": (C.c_int, [_vp]),
+    "orc_cache_max_seq_len": (C.c_int, [_vp]),
+    "orc_cache_compression_ratio": (C.c_float, [_vp]),
+    "orc_cache_weights": (_vp, [_vp, C.c_int, C.c_int]),
+    "orc_cache_scales": (_vp, [_vp, C.c_int, C.c_int]),
+    "orc_cache_biases": (_vp, [_vp, C.c_int, C.c_int]),
+    "orc_cache_max_groups": (_i64, [_vp]),
+    "orc_cache_save": (C.c_int, [_vp, C.c_char_p]),
+    "orc_cache_load": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+}
+
+_LIB = None
+_REF = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} not built (make -C oracle)")
+        h = C.CDLL(LIB_PATH)
+        for n, (r, a) in _SIG.items():
+            f = getattr(h, n)
+            f.restype, f.argtypes = r, a
+        _LIB = h
+    return _LIB
+
+
+def ref_lib():
+    """The reference's own src/ggml_type.c, built by `make -C oracle ref`
+    (None when it was not built: only where the reference sources exist)."""
+    global _REF
+    if _REF is None and os.path.exists(REF_LIB_PATH):
+        h = C.CDLL(REF_LIB_PATH)
+        h.eakv_quantize_row.restype = None
+        h.eakv_quantize_row.argtypes = [_vp, _vp, C.c_int64]
+        h.eakv_dequantize_row.restype = None
+        h.eakv_dequantize_row.argtypes = [_vp, _vp, C.c_int64]
+        h.eakv_vec_dot_q4_f32.restype = None
+        h.eakv_vec_dot_q4_f32.argtypes = [C.c_int, _vp, C.c_size_t, _vp, C.c_size_t,
+                                          _vp, C.c_size_t, C.c_int]
+        _REF = h
+    return _REF
+
+
+def _p(a):
+    return a.ctypes.data_as(_vp)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- kernels
+
+def quantize(x):
+    """x: f32[..., 64*n] -> (weights u8[n,32], scales f32[n], biases f32[n])."""
+    x = _f32(x).reshape(-1)
+    assert x.size % 64 == 0
+    n = x.size // 64
+    w = np.zeros((n, 32), np.uint8)
+    s = np.zeros(n, np.float32)
+    b = np.zeros(n, np.float32)
+    lib().orc_quantize_split(_p(x), _p(w), _p(s), _p(b), n)
+    return w, s, b
+
+
+def dequantize(w, s, b):
+    """Groups -> f32[n, 64], value j = fma(nibble_j, scale, bias)."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1, 32)
+    n = w.shape[0]
+    out = np.zeros((n, 64), np.float32)
+    lib().orc_dequantize(_p(w), _p(_f32(s)), _p(_f32(b)), _p(out), n)
+    return out
+
+
+def k_score(head_dim, q, w, s, b, seq_len, n_q, n_kv, gph):
+    q = _f32(q)
+    out = np.zeros((n_q, seq_len), np.float32)
+    lib().orc_k_score_gqa(head_dim, _p(q), _p(w), _p(_f32(s)), _p(_f32(b)), _p(out),
+                          seq_len, n_q, n_kv, gph)
+    return out
+
+
+def v_sum(head_dim, wts, w, s, b, seq_len, n_q, n_kv, gph):
+    wts = _f32(wts)
+    out = np.zeros((n_q, head_dim), np.float32)
+    lib().orc_v_sum_gqa(head_dim, _p(wts), _p(w), _p(_f32(s)), _p(_f32(b)), _p(out),
+                        seq_len, n_q, n_kv, gph)
+    return out
+
+
+def softmax_rows(scores):
+    sc = _f32(scores)
+    n, L = sc.shape
+    out = np.zeros_like(sc)
+    lib().orc_softmax_rows(_p(sc), _p(out), n, L)
+    return out
+
+
+# ---------------------------------------------------------------- cache
+
+class OracleCache:
+    """Host-memory cache: restatement of reference src/cache.c, attention.c."""
+
+    def __init__(self, n_layers, n_kv_heads, head_dim, max_seq_len, _handle=None):
+        L = lib()
+        if _handle is None:
+            _handle = L.orc_cache_create(n_layers, n_kv_heads, head_dim, max_seq_len)
+            if not _handle:
+                raise ValueError("orc_cache_create: invalid shape")
+        self.h = _handle
+
+    def free(self):
+        if self.h:
+            lib().orc_cache_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.free()
+
+    seq_len = property(lambda self: lib().orc_cache_seq_len(self.h))
+    n_layers = property(lambda self: lib().orc_cache_n_layers(self.h))
+    n_heads = property(lambda self: lib().orc_cache_n_heads(self.h))
+    head_dim = property(lambda self: lib().orc_cache_head_dim(self.h))
+    max_seq_len = property(lambda self: lib().orc_cache_max_seq_len(self.h))
+    compression_ratio = property(lambda self: lib().orc_cache_compression_ratio(self.h))
+
+    def _rc(self, rc):
+        if rc != 0:
+            raise OracleError(rc)
+        return rc
+
+    def load_raw(self, data, seq_len):
+        d = _f32(data)
+        return self._rc(lib().orc_cache_load_raw(self.h, _p(d), seq_len))
+
+    def append(self, data, layer, kv_idx, n_tokens):
+        d = _f32(data)
+        return self._rc(lib().orc_cache_append(self.h, _p(d), layer, kv_idx, n_tokens))
+
+    def advance(self, n):
+        return self._rc(lib().orc_cache_advance(self.h, n))
+
+    def clear(self):
+        lib().orc_cache_clear(self.h)
+
+    def checkpoint(self):
+        return lib().orc_checkpoint(self.h)
+
+    def restore(self, n):
+        return self._rc(lib().orc_restore(self.h, n))
+
+    def attention_scores(self, q, layer, n_q, n_kv):
+        q = _f32(q)
+        out = np.zeros((n_q, self.seq_len), np.float32)
+        lib().orc_attention_scores(self.h, _p(q), layer, n_q, n_kv, _p(out))
+        return out
+
+    def attention_output(self, w, layer, n_q, n_kv):
+        w = _f32(w)
+        out = np.zeros((n_q, self.head_dim), np.float32)
+        lib().orc_attention_output(self.h, _p(w), layer, n_q, n_kv, _p(out))
+        return out
+
+    def attention_fused(self, q, layer, n_q, n_kv):
+        q = _f32(q)
+        out = np.zeros((n_q, self.head_dim), np.float32)
+        lib().orc_attention_fused(self.h, _p(q), layer, n_q, n_kv, _p(out))
+        return out
+
+    def read_planes(self, layer, kv_idx):
+        L = lib()
+        ng = L.orc_cache_max_groups(self.h)
+        w = np.ctypeslib.as_array(C.cast(L.orc_cache_weights(self.h, layer, kv_idx),
+                                         C.POINTER(C.c_uint8)), (ng, 32)).copy()
+        s = np.ctypeslib.as_array(C.cast(L.orc_cache_scales(self.h, layer, kv_idx),
+                                         C.POINTER(C.c_float)), (ng,)).copy()
+        b = np.ctypeslib.as_array(C.cast(L.orc_cache_biases(self.h, layer, kv_idx),
+                                         C.POINTER(C.c_float)), (ng,)).copy()
+        return w, s, b
+
+    def save(self, path):
+        return self._rc(lib().orc_cache_save(self.h, os.fsencode(path)))
+
+    @classmethod
+    def load(cls, path):
+        out = _vp()
+        rc = lib().orc_cache_load(os.fsencode(path), C.byref(out))
+        if rc != 0:
+            raise OracleError(rc)
+        return cls(0, 0, 0, 0, _handle=out.value)
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code):
+        super().__init__(f"oracle error {code}")
+        self.code = code

@@ -1,0 +1,274 @@
+"""GPU parity: libeakv.so (HIP, gfx950) against the CPU oracle on the same
+seeded inputs, through the C ABI.
+
+Bar: quantization (nibbles, scales, biases) and K-scores bit-exact; V-sum and
+fused attention within |gpu - oracle| <= 1e-4 + 1e-5*|oracle|.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import tol_close
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-4, 1e-5
+
+
+@pytest.fixture(scope="module")
+def E():
+    import eakv_amd
+    from eakv_amd import hipmem
+    if hipmem.device_count() < 1:
+        pytest.fail("no HIP device visible")
+    return eakv_amd
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def special_data(rng, n_groups):
+    """Groups with NaN / inf / signed zeros / constants / tiny ranges mixed in."""
+    x = (rng.standard_normal((n_groups, 64)) *
+         np.exp(rng.uniform(-4, 4, (n_groups, 1)))).astype(np.float32)
+    k = np.arange(n_groups) % 12
+    x[k == 1, 0] = np.nan
+    x[k == 2, 17] = np.nan
+    x[k == 3] = 1.0; x[k == 3, 5] = 0.0; x[k == 3, 40] = -0.0
+    x[k == 4] = 1.0; x[k == 4, 5] = -0.0; x[k == 4, 40] = 0.0
+    x[k == 5, 9] = np.inf
+    x[k == 6, 33] = -np.inf
+    x[k == 7] = 3.25
+    x[k == 8] = 0.0; x[k == 8, 63] = np.float32(1e-45)
+    x[k == 9] = np.float32(2.0 ** -130) * rng.integers(0, 8, (np.sum(k == 9), 64))
+    x[k == 10] = -0.0
+    x[k == 11] = rng.integers(-2, 3, (np.sum(k == 11), 64))
+    return x
+
+
+def planes_equal(a, b):
+    return all(np.array_equal(np.ascontiguousarray(x).view(np.uint8),
+                              np.ascontiguousarray(y).view(np.uint8)) for x, y in zip(a, b))
+
+
+def pair(E, nl, nh, hd, lmax):
+    return E.Cache(nl, nh, hd, lmax), O.OracleCache(nl, nh, hd, lmax)
+
+
+# ------------------------------------------------------------- quantization
+
+@pytest.mark.parametrize("nl,nh,hd,L,lmax,kind", [
+    (1, 2, 128, 37, 40, "normal"), (2, 4, 64, 33, 33, "normal"),
+    (1, 1, 64, 1, 5, "normal"), (1, 3, 128, 100, 128, "special"),
+    (1, 2, 192, 10, 12, "normal"), (1, 2, 96, 7, 8, "normal"),
+    (1, 8, 128, 2048, 2048, "special"), (3, 2, 64, 513, 600, "special")])
+def test_bulk_quantize_bitexact(E, rng, nl, nh, hd, L, lmax, kind):
+    say("bulk", nl, nh, hd, L, lmax, kind)
+    n = nl * 2 * nh * L * hd
+    if kind == "normal":
+        data = rng.standard_normal(n).astype(np.float32)
+    else:
+        data = special_data(rng, n // 64).reshape(-1)
+    g, o = pair(E, nl, nh, hd, lmax)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    assert g.seq_len == L
+    for l in range(nl):
+        for kv in range(2):
+            assert planes_equal(g.read_planes(l, kv), o.read_planes(l, kv)), (l, kv)
+
+
+@pytest.mark.parametrize("hd,n_tok", [(128, 1), (64, 1), (128, 5), (64, 70)])
+def test_append_bitexact(E, rng, hd, n_tok):
+    nl, nh, lmax = 2, 4, 80
+    g, o = pair(E, nl, nh, hd, lmax)
+    base = rng.standard_normal(nl * 2 * nh * 3 * hd).astype(np.float32)
+    g.load_raw(base, 3)
+    o.load_raw(base, 3)
+    t = 3
+    while t + n_tok <= lmax:
+        for l in range(nl):
+            for kv in range(2):
+                x = special_data(rng, nh * n_tok * hd // 64).reshape(-1)
+                assert g.append(x, l, kv, n_tok) == 0
+                o.append(x, l, kv, n_tok)
+        g.advance(n_tok)
+        o.advance(n_tok)
+        t += n_tok
+        if t > 20:
+            break
+    for l in range(nl):
+        for kv in range(2):
+            assert planes_equal(g.read_planes(l, kv), o.read_planes(l, kv))
+
+
+def test_append_device_and_batch(E, rng):
+    from eakv_amd.hipmem import DeviceArray
+    nl, nh, hd, lmax, nseq = 3, 2, 128, 16, 3
+    gs = [E.Cache(nl, nh, hd, lmax) for _ in range(nseq)]
+    os_ = [O.OracleCache(nl, nh, hd, lmax) for _ in range(nseq)]
+    for i, (g, o) in enumerate(zip(gs, os_)):
+        d = rng.standard_normal(nl * 2 * nh * (4 + i) * hd).astype(np.float32)
+        dd = DeviceArray.from_host(d)
+        assert E.lib().eakv_cache_load_raw_device(g.h, dd.ptr, 4 + i, None) == 0
+        g.sync()
+        o.load_raw(d, 4 + i)
+    for step in range(3):
+        x = rng.standard_normal((nseq, nl, 2, nh, 1, hd)).astype(np.float32)
+        dx = DeviceArray.from_host(x)
+        assert E.lib().eakv_append_batch_device(E.handles(gs), nseq, dx.ptr, 1, None) == 0
+        gs[0].sync()
+        for i in range(nseq):
+            for l in range(nl):
+                for kv in range(2):
+                    os_[i].append(x[i, l, kv], l, kv, 1)
+            os_[i].advance(1)
+            gs[i].advance(1)
+    # single (layer, kv) device append
+    x = rng.standard_normal((nh, 2, hd)).astype(np.float32)
+    dx = DeviceArray.from_host(x)
+    assert E.lib().eakv_cache_append_device(gs[1].h, dx.ptr, 2, 1, 2, None) == 0
+    gs[1].sync()
+    os_[1].append(x, 2, 1, 2)
+    for g, o in zip(gs, os_):
+        for l in range(nl):
+            for kv in range(2):
+                assert planes_equal(g.read_planes(l, kv), o.read_planes(l, kv))
+
+
+# ------------------------------------------------------------- attention
+
+SHAPES = [  # (n_kv heads in cache, n_q, n_kv used, d, L, lmax)
+    (8, 8, 8, 128, 37, 40), (4, 32, 4, 64, 300, 300), (8, 32, 8, 128, 513, 520),
+    (2, 16, 2, 128, 1000, 1024), (4, 4, 4, 64, 1, 4), (4, 8, 2, 128, 257, 260),
+    (1, 8, 1, 64, 1025, 1030), (2, 64, 2, 128, 100, 100)]
+
+
+def loaded(E, rng, nh, d, L, lmax, nl=2):
+    g, o = pair(E, nl, nh, d, lmax)
+    data = (rng.standard_normal(nl * 2 * nh * L * d) * 1.5).astype(np.float32)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    return g, o
+
+
+@pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", SHAPES)
+def test_k_score_bitexact(E, rng, nh, n_q, n_kv, d, L, lmax):
+    say("kscore", nh, n_q, n_kv, d, L)
+    g, o = loaded(E, rng, nh, d, L, lmax)
+    q = rng.standard_normal((n_q, d)).astype(np.float32)
+    for layer in (0, 1):
+        a = g.attention_scores(q, layer, n_q, n_kv)
+        b = o.attention_scores(q, layer, n_q, n_kv)
+        assert a.shape == (n_q, L)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
+            np.abs(a - b).max()
+
+
+@pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", SHAPES)
+def test_v_sum_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
+    say("vsum", nh, n_q, n_kv, d, L)
+    g, o = loaded(E, rng, nh, d, L, lmax)
+    q = rng.standard_normal((n_q, d)).astype(np.float32)
+    w = O.softmax_rows(o.attention_scores(q, 1, n_q, n_kv))
+    a = g.attention_output(w, 1, n_q, n_kv)
+    b = o.attention_output(w, 1, n_q, n_kv)
+    ok, err, nbad = tol_close(a, b, ATOL, RTOL)
+    assert ok, (err, nbad)
+    # unnormalised weights too
+    w2 = rng.random((n_q, L)).astype(np.float32)
+    ok, err, nbad = tol_close(g.attention_output(w2, 1, n_q, n_kv),
+                              o.attention_output(w2, 1, n_q, n_kv), ATOL, RTOL)
+    assert ok, (err, nbad)
+
+
+@pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", SHAPES)
+def test_fused_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
+    say("fused", nh, n_q, n_kv, d, L)
+    g, o = loaded(E, rng, nh, d, L, lmax)
+    q = (rng.standard_normal((n_q, d)) * 2).astype(np.float32)
+    a = g.attention_fused(q, 1, n_q, n_kv)
+    b = o.attention_fused(q, 1, n_q, n_kv)
+    ok, err, nbad = tol_close(a, b, ATOL, RTOL)
+    assert ok, (err, nbad)
+
+
+def test_fused_batch_device(E, rng):
+    from eakv_amd.hipmem import DeviceArray
+    nl, nh, d, n_q, lmax = 2, 4, 128, 16, 1100
+    lens = [1, 511, 512, 513, 1100, 37]
+    gs, os_ = [], []
+    for L in lens:
+        g, o = loaded(E, rng, nh, d, L, lmax, nl)
+        gs.append(g)
+        os_.append(o)
+    q = rng.standard_normal((len(lens), n_q, d)).astype(np.float32)
+    dq = DeviceArray.from_host(q)
+    dout = DeviceArray((len(lens), n_q, d))
+    assert E.lib().eakv_attention_fused_batch_device(E.handles(gs), len(gs), 1, dq.ptr,
+                                                     n_q, nh, dout.ptr, None) == 0
+    gs[0].sync()
+    out = dout.download()
+    for i, o in enumerate(os_):
+        ok, err, nbad = tol_close(out[i], o.attention_fused(q[i], 1, n_q, nh), ATOL, RTOL)
+        assert ok, (lens[i], err, nbad)
+
+
+def test_device_calls_equal_host_calls(E, rng):
+    from eakv_amd.hipmem import DeviceArray
+    g, _ = loaded(E, rng, 4, 128, 200, 256)
+    q = rng.standard_normal((16, 128)).astype(np.float32)
+    dq, ds = DeviceArray.from_host(q), DeviceArray((16, 200))
+    assert E.lib().eakv_attention_scores_device(g.h, dq.ptr, 0, 16, 4, ds.ptr, None) == 0
+    g.sync()
+    assert np.array_equal(ds.download(), g.attention_scores(q, 0, 16, 4))
+    w = rng.random((16, 200)).astype(np.float32)
+    dw, do = DeviceArray.from_host(w), DeviceArray((16, 128))
+    assert E.lib().eakv_attention_output_device(g.h, dw.ptr, 0, 16, 4, do.ptr, None) == 0
+    g.sync()
+    assert np.array_equal(do.download(), g.attention_output(w, 0, 16, 4))
+
+
+def test_empty_cache(E):
+    g, o = pair(E, 1, 2, 64, 8)
+    q = np.ones((2, 64), np.float32)
+    assert g.attention_scores(q, 0, 2, 2).shape == (2, 0)
+    out = g.attention_output(np.zeros((2, 0), np.float32), 0, 2, 2)
+    assert np.array_equal(out, o.attention_output(np.zeros((2, 0), np.float32), 0, 2, 2))
+    assert not out.any()
+    assert np.isnan(g.attention_fused(q, 0, 2, 2)).all()
+
+
+@pytest.mark.parametrize("args", [(0, 3, 2), (0, 4, 3), (2, 4, 4), (0, 16, 8), (-1, 4, 4)])
+def test_attention_rejects_invalid(E, rng, args):
+    layer, n_q, n_kv = args
+    g, _ = loaded(E, rng, 4, 64, 10, 10)
+    with pytest.raises(E.EakvError) as e:
+        g.attention_scores(np.ones((n_q, 64), np.float32), layer, n_q, n_kv)
+    assert e.value.code == E.EAKV_ERR_INVALID
+
+
+def test_head_dim_other_than_64_128_rejected(E, rng):
+    g = E.Cache(1, 2, 192, 8)
+    g.load_raw(rng.standard_normal(2 * 2 * 8 * 192).astype(np.float32), 8)
+    with pytest.raises(E.EakvError):
+        g.attention_scores(np.ones((2, 192), np.float32), 0, 2, 2)
+
+
+def test_save_bytes_match_oracle(E, rng, tmp_path):
+    for (nl, nh, hd, L, lmax) in [(2, 4, 128, 32, 32), (1, 3, 64, 10, 16)]:
+        g, o = pair(E, nl, nh, hd, lmax)
+        data = rng.standard_normal(nl * 2 * nh * L * hd).astype(np.float32)
+        g.load_raw(data, L)
+        o.load_raw(data, L)
+        pg, po = tmp_path / "g.eakv", tmp_path / "o.eakv"
+        g.save(str(pg))
+        o.save(str(po))
+        assert pg.read_bytes() == po.read_bytes()
+        h = E.Cache.load(str(po))
+        q = rng.standard_normal((nh, hd)).astype(np.float32)
+        assert np.array_equal(h.attention_scores(q, 0, nh, nh), o.attention_scores(q, 0, nh, nh))
