@@ -212,7 +212,8 @@ def cpu_baseline(cfg, budget_s=12.0):
     oc.attention_fused(q, 0, nq, nkv)
     single = time.perf_counter() - t0
     threads = max(1, min(16, os.cpu_count() or 1))
-    reps = max(1, int(budget_s / max(single, 1e-3) / 2))
+    # one unit per thread, more while the budget allows
+    reps = threads * max(1, int(budget_s / max(single, 1e-3) / 2))
     reps = min(reps, 4 * threads)
     t0 = time.perf_counter()
     with ThreadPoolExecutor(threads) as ex:
