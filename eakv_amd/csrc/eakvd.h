@@ -98,9 +98,13 @@ typedef struct {
 
 size_t eakvd_fused_work_bytes(const eakvd_geom *g, const eakvd_batch *b,
                               int n_q);
+/* counters: EAKVD_MAX_BATCH*n_kv_heads u32, all zero on entry; the launch
+ * leaves them zero again (the last block of each (sequence, kv head) resets
+ * its own).  Launches that share a counter array must not overlap. */
+#define EAKVD_COUNTERS(n_kv_heads) ((size_t)EAKVD_MAX_BATCH * (n_kv_heads))
 int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
                 const float *q, int n_q, int n_kv, float *out, void *work,
-                void *stream);
+                unsigned *counters, void *stream);
 
 #ifdef __cplusplus
 }

@@ -64,3 +64,8 @@ __device__ __forceinline__ float wave_sum(float v)
 }
 
 static inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+#define EAKV_LOG2E 1.4426950408889634f

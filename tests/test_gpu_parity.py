@@ -145,7 +145,9 @@ def test_append_device_and_batch(E, rng):
 SHAPES = [  # (n_kv heads in cache, n_q, n_kv used, d, L, lmax)
     (8, 8, 8, 128, 37, 40), (4, 32, 4, 64, 300, 300), (8, 32, 8, 128, 513, 520),
     (2, 16, 2, 128, 1000, 1024), (4, 4, 4, 64, 1, 4), (4, 8, 2, 128, 257, 260),
-    (1, 8, 1, 64, 1025, 1030), (2, 64, 2, 128, 100, 100)]
+    (1, 8, 1, 64, 1025, 1030), (2, 64, 2, 128, 100, 100),
+    (8, 32, 8, 128, 4097, 4100), (4, 16, 4, 64, 2049, 2050), (2, 4, 2, 128, 3000, 3000),
+    (2, 6, 2, 64, 700, 704)]
 
 
 def loaded(E, rng, nh, d, L, lmax, nl=2):
@@ -272,3 +274,31 @@ def test_save_bytes_match_oracle(E, rng, tmp_path):
         h = E.Cache.load(str(po))
         q = rng.standard_normal((nh, hd)).astype(np.float32)
         assert np.array_equal(h.attention_scores(q, 0, nh, nh), o.attention_scores(q, 0, nh, nh))
+
+
+@pytest.mark.parametrize("d,n_q,n_kv,L", [(128, 32, 8, 5000), (64, 32, 4, 3000),
+                                          (128, 32, 32, 2100), (128, 64, 8, 2500)])
+def test_fused_parity_config_distributions(E, rng, d, n_q, n_kv, L):
+    """Channel scales log-uniform in [0.5, 4] with two x10 outlier channels per
+    head (K), and 1% +-20 outliers (V): the magnitudes of the benchmark
+    configurations, at a context the oracle finishes quickly."""
+    say("fused-dist", d, n_q, n_kv, L)
+    nl = 1
+    ch = np.exp(rng.uniform(np.log(0.5), np.log(4.0), (n_kv, d))).astype(np.float32)
+    for h in range(n_kv):
+        ch[h, rng.choice(d, 2, replace=False)] *= 10
+    K = rng.standard_normal((n_kv, L, d)).astype(np.float32) * ch[:, None, :]
+    V = rng.standard_normal((n_kv, L, d)).astype(np.float32)
+    out_mask = rng.random(V.shape) < 0.01
+    V[out_mask] = np.where(rng.random(out_mask.sum()) < 0.5, -20.0, 20.0)
+    data = np.stack([K, V])[None].astype(np.float32)
+    g, o = pair(E, nl, n_kv, d, L + 8)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    q = rng.standard_normal((n_q, d)).astype(np.float32)
+    a = g.attention_fused(q, 0, n_q, n_kv)
+    b = o.attention_fused(q, 0, n_q, n_kv)
+    ok, err, nbad = tol_close(a, b, ATOL, RTOL)
+    assert ok, (err, nbad)
+    sa = g.attention_scores(q, 0, n_q, n_kv)
+    assert np.array_equal(sa, o.attention_scores(q, 0, n_q, n_kv))
