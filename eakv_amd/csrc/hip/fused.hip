@@ -34,8 +34,10 @@ namespace {
 // ------------------------------------------------------------------ MFMA
 
 constexpr int kWaves = 4;
-constexpr int kTW = 512;                // tokens per wave per chunk
+constexpr int kTW = 1024;               // tokens per wave per chunk
 constexpr int kChunkM = kWaves * kTW;   // tokens per block
+constexpr int kTT = 64;                 // tokens per tile (one pipeline stage)
+constexpr float kTau = 8.0f;            // lazy-rescale headroom, e^8
 
 __device__ __forceinline__ int sext8(int v) { return (int)(int8_t)(v & 0xff); }
 
@@ -52,16 +54,67 @@ __device__ __forceinline__ int digit_of(int z, int p)
     return p == 0 ? d3 : (p == 1 ? d2 : (p == 2 ? d1 : d0));
 }
 
+// One lane's share of a kTT-token tile: the packed K bytes and K scale/bias
+// of its MFMA sub-tiles, and the packed V bytes and V scale/bias of its
+// V steps.
 template <int D>
-__global__ __launch_bounds__(256) void mfma_kernel(
+struct Tile {
+    static constexpr int GPD = D / 64;
+    static constexpr int NK = kTT / 16;          // K sub-tiles of 16 tokens
+    static constexpr int TS = 16 / GPD;          // V token slots per step
+    static constexpr int NV = kTT / TS;          // V steps
+    uint2 kw[NK][GPD];
+    float ks[NK][GPD], kb[NK][GPD];
+    uint2 vw[NV];
+    float vs[NV], vb[NV];
+};
+
+template <int D>
+__device__ __forceinline__ void load_tile(Tile<D> &T, const Planes &K,
+                                          const Planes &V, int64_t hbase,
+                                          int t, int we, int tl, int qq,
+                                          int ts, int grp, int x)
+{
+    constexpr int GPD = D / 64;
+#pragma unroll
+    for (int k = 0; k < Tile<D>::NK; k++) {
+        const int tok = min(t + 16 * k + tl, we - 1);
+        const int64_t gk = hbase + (int64_t)tok * GPD;
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++)
+            T.kw[k][gg] = *reinterpret_cast<const uint2 *>(K.w + (gk + gg) * 32 + qq * 8);
+        if (GPD == 2) {
+            const float2 sv = *reinterpret_cast<const float2 *>(K.s + gk);
+            const float2 bv = *reinterpret_cast<const float2 *>(K.b + gk);
+            T.ks[k][0] = sv.x; T.ks[k][GPD - 1] = sv.y;
+            T.kb[k][0] = bv.x; T.kb[k][GPD - 1] = bv.y;
+        } else {
+            T.ks[k][0] = K.s[gk];
+            T.kb[k][0] = K.b[gk];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < Tile<D>::NV; j++) {
+        const int tok = min(t + Tile<D>::TS * j + ts, we - 1);
+        const int64_t gv = hbase + (int64_t)tok * GPD + grp;
+        T.vw[j] = *reinterpret_cast<const uint2 *>(V.w + gv * 32 + x * 8);
+        T.vs[j] = V.s[gv];
+        T.vb[j] = V.b[gv];
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
     int n_q, int qpk, int n_kv, int max_chunks, float rs,
     float *__restrict__ part, unsigned *__restrict__ cnt,
     float *__restrict__ out)
 {
     constexpr int GPD = D / 64;
-    constexpr int TS = 16 / GPD;  // V token slots per step
-    __shared__ float s_lds[kWaves][4][kTW];
+    constexpr int TS = Tile<D>::TS;
+    constexpr int NK = Tile<D>::NK;
+    constexpr int NV = Tile<D>::NV;
+    __shared__ float p_lds[kWaves][2][4][kTT];
     __shared__ float o_lds[kWaves][4][D];
     __shared__ float m_lds[kWaves][4], l_lds[kWaves][4];
     __shared__ int last_flag;
@@ -82,6 +135,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(
     const int we = min(L, wb + kTW);
     const Planes K = planes_of(g, bt.base[s], layer, 0);
     const Planes V = planes_of(g, bt.base[s], layer, 1);
+    const int64_t hbase = (int64_t)kvh * g.gph;
     const float *qs = q + ((int64_t)s * n_q + (int64_t)kvh * qpk) * D;
 
     // ---- q -> A operands.  Lane l: row i = l%16 (head ha = i/4, digit
@@ -122,82 +176,108 @@ __global__ __launch_bounds__(256) void mfma_kernel(
         qsum[gg] += __shfl_xor(qsum[gg], 32, 64);
     }
     // constants of the head whose scores this lane receives (ho = l/16)
-    const int ho = l >> 4;
+    const int ho = l >> 4, tl = l & 15;
     const int esh_o = __shfl(esh, 4 * ho, 64);
     const double cs = (double)rs * ldexp(1.0, -esh_o);
     double bq[GPD];
 #pragma unroll
     for (int gg = 0; gg < GPD; gg++) bq[gg] = (double)rs * __shfl(qsum[gg], 4 * ho, 64);
 
-    // ---- K phase
-    float mloc = -INFINITY;
-    const int tl = l & 15;
-    for (int t = wb; t < we; t += 16) {
-        const int tok = t + tl;
-        const int tk = tok < we ? tok : we - 1;
-        const int64_t gk = (int64_t)kvh * g.gph + (int64_t)tk * GPD;
-        double acc = 0.0;
-        float sk[GPD], bk[GPD];
-        if (GPD == 2) {
-            const float2 sv = *reinterpret_cast<const float2 *>(K.s + gk);
-            const float2 bv = *reinterpret_cast<const float2 *>(K.b + gk);
-            sk[0] = sv.x; sk[GPD - 1] = sv.y;
-            bk[0] = bv.x; bk[GPD - 1] = bv.y;
-        } else {
-            sk[0] = K.s[gk];
-            bk[0] = K.b[gk];
-        }
-#pragma unroll
-        for (int gg = 0; gg < GPD; gg++) {
-            const uint2 raw =
-                *reinterpret_cast<const uint2 *>(K.w + (gk + gg) * 32 + qq * 8);
-            const v4i B = v4i{(int)(raw.x & 0x0F0F0F0Fu), (int)(raw.y & 0x0F0F0F0Fu),
-                              (int)((raw.x >> 4) & 0x0F0F0F0Fu),
-                              (int)((raw.y >> 4) & 0x0F0F0F0Fu)};
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[gg], B, v4i{0, 0, 0, 0},
-                                                                0, 0, 0);
-            const double dot = ((double)d[0] * 16777216.0 + (double)d[1] * 65536.0) +
-                               ((double)d[2] * 256.0 + (double)d[3]);
-            acc += cs * ((double)sk[gg] * dot) + (double)bk[gg] * bq[gg];
-        }
-        const float sc = tok < we ? (float)acc : -INFINITY;
-        s_lds[w][ho][tok - wb] = sc;
-        mloc = fmaxf(mloc, sc);
-    }
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
-    __syncthreads();
-
-    // ---- V phase.  Lane l = grp*4*TS + ts*4 + x: block (grp, ts) = token
-    // slot ts of group grp; x = head (A rows) and dim column (B).  Column x of
+    // V lane roles: l = grp*4*TS + ts*4 + x; block (grp, ts) = token slot ts
+    // of group grp, x = head (A row) and dim column (B).  Column x of
     // accumulator m is dim 64grp + 32(m>=8) + 8x + m%8.
     const int x = l & 3, ts = (l >> 2) % TS, grp = (l >> 2) / TS;
-    const float mx = __shfl(mloc, 16 * x, 64);
+
     v4f acc[16];
 #pragma unroll
     for (int m = 0; m < 16; m++) acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     float bacc = 0.0f, lsum = 0.0f;
-    for (int t = wb; t < we; t += TS) {
-        const int tok = t + ts;
-        const bool valid = tok < we && x < G;
-        const int tk = tok < we ? tok : we - 1;
-        const int64_t gv = (int64_t)kvh * g.gph + (int64_t)tk * GPD + grp;
-        const uint2 raw = *reinterpret_cast<const uint2 *>(V.w + gv * 32 + x * 8);
-        const float sv = V.s[gv], bv = V.b[gv];
-        const float sc = s_lds[w][x][tok - wb];
-        const float p = valid ? exp2f((sc - mx) * EAKV_LOG2E) : 0.0f;
-        const float a = p * sv;
-        bacc = fmaf(p, bv, bacc);
-        lsum += grp == 0 ? p : 0.0f;
-        const uint32_t lo0 = raw.x & 0x0F0F0F0Fu, lo1 = raw.y & 0x0F0F0F0Fu;
-        const uint32_t hi0 = (raw.x >> 4) & 0x0F0F0F0Fu, hi1 = (raw.y >> 4) & 0x0F0F0F0Fu;
+    float mrun[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+
+    Tile<D> cur, nxt;
+    if (wb < we) load_tile<D>(cur, K, V, hbase, wb, we, tl, qq, ts, grp, x);
+    int buf = 0;
+    for (int t = wb; t < we; t += kTT) {
+        if (t + kTT < we) load_tile<D>(nxt, K, V, hbase, t + kTT, we, tl, qq, ts, grp, x);
+
+        // ---- K: scores of this lane's head ho for tokens t + 16k + tl
+        float sc[NK];
+        float mt = -INFINITY;
 #pragma unroll
-        for (int m = 0; m < 16; m++) {
-            const uint32_t wd = m < 8 ? (m < 4 ? lo0 : lo1) : (m < 12 ? hi0 : hi1);
-            const float nb = (float)((wd >> (8 * (m & 3))) & 0xffu);
-            acc[m] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, nb, acc[m], 0, 0, 0);
+        for (int k = 0; k < NK; k++) {
+            double a = 0.0;
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) {
+                const uint2 raw = cur.kw[k][gg];
+                const v4i B = v4i{(int)(raw.x & 0x0F0F0F0Fu), (int)(raw.y & 0x0F0F0F0Fu),
+                                  (int)((raw.x >> 4) & 0x0F0F0F0Fu),
+                                  (int)((raw.y >> 4) & 0x0F0F0F0Fu)};
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[gg], B,
+                                                                    v4i{0, 0, 0, 0}, 0, 0, 0);
+                const double dot = ((double)d[0] * 16777216.0 + (double)d[1] * 65536.0) +
+                                   ((double)d[2] * 256.0 + (double)d[3]);
+                a += cs * ((double)cur.ks[k][gg] * dot) + (double)cur.kb[k][gg] * bq[gg];
+            }
+            sc[k] = t + 16 * k + tl < we ? (float)a : -INFINITY;
+            mt = fmaxf(mt, sc[k]);
         }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, 64));
+
+        // ---- lazy rescale: move the running max only when a head's tile max
+        // exceeds it by more than kTau, so p = exp(s - mrun) stays <= e^kTau
+        float mth[4];
+        bool up = false;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            mth[r] = __shfl(mt, 16 * r, 64);
+            up |= mth[r] > mrun[r] + kTau;
+        }
+        if (up) {
+            float f[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float mn = mth[r] > mrun[r] + kTau ? mth[r] : mrun[r];
+                f[r] = exp2f((mrun[r] - mn) * EAKV_LOG2E);
+                mrun[r] = mn;
+            }
+#pragma unroll
+            for (int m = 0; m < 16; m++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[m][r] *= f[r];
+            const float fx = x == 0 ? f[0] : (x == 1 ? f[1] : (x == 2 ? f[2] : f[3]));
+            bacc *= fx;
+            lsum *= fx;
+        }
+        const float mho = ho == 0 ? mrun[0] : (ho == 1 ? mrun[1] : (ho == 2 ? mrun[2] : mrun[3]));
+#pragma unroll
+        for (int k = 0; k < NK; k++)
+            p_lds[w][buf][ho][16 * k + tl] = exp2f((sc[k] - mho) * EAKV_LOG2E);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // ---- V: p*scale rows x 4 dims columns per 4x4x1 block
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const float p = x < G ? p_lds[w][buf][x][TS * j + ts] : 0.0f;
+            const float a = p * cur.vs[j];
+            bacc = fmaf(p, cur.vb[j], bacc);
+            lsum += grp == 0 ? p : 0.0f;
+            const uint2 raw = cur.vw[j];
+            const uint32_t lo0 = raw.x & 0x0F0F0F0Fu, lo1 = raw.y & 0x0F0F0F0Fu;
+            const uint32_t hi0 = (raw.x >> 4) & 0x0F0F0F0Fu, hi1 = (raw.y >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int m = 0; m < 16; m++) {
+                const uint32_t wd = m < 8 ? (m < 4 ? lo0 : lo1) : (m < 12 ? hi0 : hi1);
+                const float nb = (float)((wd >> (8 * (m & 3))) & 0xffu);
+                acc[m] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, nb, acc[m], 0, 0, 0);
+            }
+        }
+        cur = nxt;
+        buf ^= 1;
     }
+
     // sum the token slots (lane bits 2 .. 2+log2(TS)-1)
 #pragma unroll
     for (int o = 4; o < 4 * TS; o <<= 1) {
@@ -220,7 +300,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(
         }
     }
     if (l < 4) {
-        m_lds[w][l] = mx;
+        m_lds[w][l] = mrun[l];
         l_lds[w][l] = lsum;
     }
     __syncthreads();

@@ -181,11 +181,18 @@ def test_v_sum_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
     b = o.attention_output(w, 1, n_q, n_kv)
     ok, err, nbad = tol_close(a, b, ATOL, RTOL)
     assert ok, (err, nbad)
-    # unnormalised weights too
+    # Unnormalised weights: a plain f32 sum of seq_len terms, whose rounding
+    # (oracle: one sequential chain; GPU: split chains) grows with the sum of
+    # |terms|.  Both are held to 4e-7 * sum|w*v| + 1e-4 of the exact f64 value.
     w2 = rng.random((n_q, L)).astype(np.float32)
-    ok, err, nbad = tol_close(g.attention_output(w2, 1, n_q, n_kv),
-                              o.attention_output(w2, 1, n_q, n_kv), ATOL, RTOL)
-    assert ok, (err, nbad)
+    vw, vs, vb = o.read_planes(1, 1)
+    Vd = O.dequantize(vw, vs, vb).reshape(nh, lmax, d)[:n_kv, :L].astype(np.float64)
+    Vd = np.repeat(Vd, n_q // n_kv, axis=0)
+    exact = np.einsum("ht,htd->hd", w2.astype(np.float64), Vd)
+    mag = np.einsum("ht,htd->hd", w2.astype(np.float64), np.abs(Vd))
+    for got in (g.attention_output(w2, 1, n_q, n_kv), o.attention_output(w2, 1, n_q, n_kv)):
+        err = np.abs(got - exact)
+        assert np.all(err <= 1e-4 + 4e-7 * mag), (err.max(), (err / mag).max())
 
 
 @pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", SHAPES)
