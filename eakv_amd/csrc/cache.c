@@ -121,7 +121,7 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
     c->head_dim = head_dim;
     c->max_seq_len = max_seq_len;
     eakvd_geom_init(&c->geom, n_layers, n_kv_heads, head_dim, max_seq_len);
-    c->dev_bytes = (size_t)c->geom.block_bytes * 2 * (size_t)n_layers;
+    c->dev_bytes = (size_t)c->geom.block_bytes * 2 * (size_t)n_layers + EAKVD_TAIL_PAD;
 
     int e = eakvd_get_device(&c->device);
     if (e) goto hip_fail;

@@ -23,6 +23,11 @@ extern "C" {
 /* Sequences per batched launch (kernel-argument arrays). */
 #define EAKVD_MAX_BATCH 32
 
+/* Bytes allocated after a cache's last plane: the fused kernel reads whole
+ * tiles (at most 64 tokens of K and V, 64 B each, and their scales) past a
+ * sequence's last token and masks them. */
+#define EAKVD_TAIL_PAD (64 * 1024)
+
 typedef struct {
     int     n_layers, n_kv_heads, head_dim, max_seq_len;
     int64_t gpd;          /* groups per token per head */

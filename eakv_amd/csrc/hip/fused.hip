@@ -36,7 +36,10 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kTW = 1024;               // tokens per wave per chunk
 constexpr int kChunkM = kWaves * kTW;   // tokens per block
-constexpr int kTT = 64;                 // tokens per tile (one pipeline stage)
+#ifndef EAKV_FUSED_TT
+#define EAKV_FUSED_TT 32
+#endif
+constexpr int kTT = EAKV_FUSED_TT;      // tokens per tile (one pipeline stage)
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, e^8
 
 __device__ __forceinline__ int sext8(int v) { return (int)(int8_t)(v & 0xff); }
@@ -69,37 +72,214 @@ struct Tile {
     float vs[NV], vb[NV];
 };
 
+// Buffer resources of the six planes (scalar registers) and this lane's byte
+// offsets at the wave's first token.  A tile is read with buffer loads:
+// resource + lane offset + uniform tile offset + immediate, so a tile costs
+// no per-lane address arithmetic.  Reads past a plane's end return 0.
+struct LaneOffs {
+    __amdgpu_buffer_rsrc_t kw, vw, ks, kb, vs, vb;
+    uint32_t kwo, kso, vwo, vso;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void *p, int64_t bytes)
+{
+    // dword3 0x00020000: raw (untyped) 32-bit buffer on gfx9-family parts
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint2 ldb64(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)vo, (int)so, 0);
+    return uint2{v[0], v[1]};
+}
+
+__device__ __forceinline__ float ldf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so)
+{
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0));
+}
+
+// The tile at token offset dt of the wave.  A tile can run up to kTT - 1
+// tokens past the wave's last token; those reads stay inside the plane (or
+// return 0 beyond it) and their scores are masked to -inf, so their weight is
+// exactly 0.
 template <int D>
-__device__ __forceinline__ void load_tile(Tile<D> &T, const Planes &K,
-                                          const Planes &V, int64_t hbase,
-                                          int t, int we, int tl, int qq,
-                                          int ts, int grp, int x)
+__device__ __forceinline__ void load_tile(Tile<D> &T, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
+    constexpr int TS = Tile<D>::TS;
+    // dt is the same in every lane; readfirstlane makes that visible, so the
+    // tile offsets go to the scalar soffset operand
+    const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
+    const uint32_t ws = du * GPD * 32, ss = du * GPD * 4;
 #pragma unroll
     for (int k = 0; k < Tile<D>::NK; k++) {
-        const int tok = min(t + 16 * k + tl, we - 1);
-        const int64_t gk = hbase + (int64_t)tok * GPD;
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
-            T.kw[k][gg] = *reinterpret_cast<const uint2 *>(K.w + (gk + gg) * 32 + qq * 8);
+            T.kw[k][gg] = ldb64(P.kw, P.kwo + (16 * k * GPD + gg) * 32, ws);
         if (GPD == 2) {
-            const float2 sv = *reinterpret_cast<const float2 *>(K.s + gk);
-            const float2 bv = *reinterpret_cast<const float2 *>(K.b + gk);
-            T.ks[k][0] = sv.x; T.ks[k][GPD - 1] = sv.y;
-            T.kb[k][0] = bv.x; T.kb[k][GPD - 1] = bv.y;
+            const uint2 sv = ldb64(P.ks, P.kso + 16 * k * GPD * 4, ss);
+            const uint2 bv = ldb64(P.kb, P.kso + 16 * k * GPD * 4, ss);
+            T.ks[k][0] = __uint_as_float(sv.x); T.ks[k][GPD - 1] = __uint_as_float(sv.y);
+            T.kb[k][0] = __uint_as_float(bv.x); T.kb[k][GPD - 1] = __uint_as_float(bv.y);
         } else {
-            T.ks[k][0] = K.s[gk];
-            T.kb[k][0] = K.b[gk];
+            T.ks[k][0] = ldf(P.ks, P.kso + 16 * k * 4, ss);
+            T.kb[k][0] = ldf(P.kb, P.kso + 16 * k * 4, ss);
         }
     }
 #pragma unroll
     for (int j = 0; j < Tile<D>::NV; j++) {
-        const int tok = min(t + Tile<D>::TS * j + ts, we - 1);
-        const int64_t gv = hbase + (int64_t)tok * GPD + grp;
-        T.vw[j] = *reinterpret_cast<const uint2 *>(V.w + gv * 32 + x * 8);
-        T.vs[j] = V.s[gv];
-        T.vb[j] = V.b[gv];
+        T.vw[j] = ldb64(P.vw, P.vwo + TS * j * GPD * 32, ws);
+        T.vs[j] = ldf(P.vs, P.vso + TS * j * GPD * 4, ss);
+        T.vb[j] = ldf(P.vb, P.vso + TS * j * GPD * 4, ss);
+    }
+}
+
+// State carried across the tiles of one wave.  The running maxima are
+// wave-uniform scalars.
+template <int D>
+struct WaveState {
+    v4f acc[16];
+    float bacc, lsum;
+    float m0, m1, m2, m3;
+};
+
+__device__ __forceinline__ float sel4(int i, float a, float b, float c, float d)
+{
+    float r = a;
+    r = i == 1 ? b : r;
+    r = i == 2 ? c : r;
+    r = i == 3 ? d : r;
+    return r;
+}
+
+// x & 0x0F0F0F0F hidden from the optimizer, so that extracting byte k of the
+// result stays one v_cvt_f32_ubyte<k>
+__device__ __forceinline__ uint32_t nib_lo(uint32_t x)
+{
+    uint32_t r;
+    asm volatile("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t nib_hi(uint32_t x)
+{
+    uint32_t r;
+    asm volatile("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(x >> 4));
+    return r;
+}
+
+__device__ __forceinline__ float row_max16(float v)
+{
+    // max over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1)
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false)));
+    return v;
+}
+
+template <int D>
+__device__ __forceinline__ void process_tile(
+    WaveState<D> &S, const Tile<D> &T, int dt, int n_tok, const v4i *A,
+    const float *wsc, const float *bq, float (*pl)[kTT], int G, int ho,
+    int tl, int ts, int x)
+{
+    constexpr int GPD = D / 64;
+    constexpr int TS = Tile<D>::TS;
+    constexpr int NK = Tile<D>::NK;
+    constexpr int NV = Tile<D>::NV;
+
+    // ---- K: per sub-tile, the digit-row dots of both groups, then their
+    // recombination: the exact integer dot of each digit row times its
+    // weight (wsc holds 2^24, 2^16, 2^8, 1 times 2^-e/sqrt(d)), in f32.
+    float sc[NK];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NK; k++) {
+        v4i d[GPD];
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) {
+            const uint2 raw = T.kw[k][gg];
+            const v4i B = v4i{(int)nib_lo(raw.x), (int)nib_lo(raw.y), (int)nib_hi(raw.x),
+                              (int)nib_hi(raw.y)};
+            d[gg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[gg], B, v4i{0, 0, 0, 0}, 0, 0, 0);
+        }
+        float a = 0.0f;
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) {
+            float u = (float)d[gg][3] * wsc[3];
+            u = fmaf((float)d[gg][2], wsc[2], u);
+            u = fmaf((float)d[gg][1], wsc[1], u);
+            u = fmaf((float)d[gg][0], wsc[0], u);
+            a = fmaf(T.ks[k][gg], u, fmaf(T.kb[k][gg], bq[gg], a));
+        }
+        sc[k] = dt + 16 * k + tl < n_tok ? a : -INFINITY;
+        mt = fmaxf(mt, sc[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    mt = row_max16(mt);
+
+    // ---- lazy rescale: move the running max only when a head's tile max
+    // exceeds it by more than kTau, so p = exp(s - mrun) stays <= e^kTau
+    const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 0));
+    const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 16));
+    const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 32));
+    const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 48));
+    const bool u0 = t0 > S.m0 + kTau, u1 = t1 > S.m1 + kTau;
+    const bool u2 = t2 > S.m2 + kTau, u3 = t3 > S.m3 + kTau;
+    if (u0 || u1 || u2 || u3) {
+        const float n0 = u0 ? t0 : S.m0, n1 = u1 ? t1 : S.m1;
+        const float n2 = u2 ? t2 : S.m2, n3 = u3 ? t3 : S.m3;
+        const float f0 = exp2f((S.m0 - n0) * EAKV_LOG2E), f1 = exp2f((S.m1 - n1) * EAKV_LOG2E);
+        const float f2 = exp2f((S.m2 - n2) * EAKV_LOG2E), f3 = exp2f((S.m3 - n3) * EAKV_LOG2E);
+        S.m0 = n0; S.m1 = n1; S.m2 = n2; S.m3 = n3;
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+            S.acc[m][0] *= f0;
+            S.acc[m][1] *= f1;
+            S.acc[m][2] *= f2;
+            S.acc[m][3] *= f3;
+        }
+        S.bacc *= sel4(x, f0, f1, f2, f3);
+        S.lsum *= sel4(ho, f0, f1, f2, f3);
+    }
+    // p in the score layout (head ho, token 16k + tl); heads >= G get 0
+    const float mho = sel4(ho, S.m0, S.m1, S.m2, S.m3);
+#pragma unroll
+    for (int k = 0; k < NK; k++) {
+        const float p = ho < G ? exp2f((sc[k] - mho) * EAKV_LOG2E) : 0.0f;
+        S.lsum += p;
+        pl[ho][16 * k + tl] = p;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- V: rows p*scale (4 heads) x columns 4 dims per 4x4x1 block
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const float p = pl[x][TS * j + ts];
+        const float a = p * T.vs[j];
+        S.bacc = fmaf(p, T.vb[j], S.bacc);
+        const uint2 raw = T.vw[j];
+        // low nibbles (accumulators 0-7), then high nibbles (8-15)
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const uint32_t w0 = half ? nib_hi(raw.x) : nib_lo(raw.x);
+            const uint32_t w1 = half ? nib_hi(raw.y) : nib_lo(raw.y);
+            float nb[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                nb[e] = (float)(((e < 4 ? w0 : w1) >> (8 * (e & 3))) & 0xffu);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                S.acc[8 * half + e] =
+                    __builtin_amdgcn_mfma_f32_4x4x1f32(a, nb[e], S.acc[8 * half + e], 0, 0, 0);
+        }
+        // keep the steps apart: hoisting later steps' conversions above these
+        // MFMAs only raises register pressure
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -112,8 +292,6 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
 {
     constexpr int GPD = D / 64;
     constexpr int TS = Tile<D>::TS;
-    constexpr int NK = Tile<D>::NK;
-    constexpr int NV = Tile<D>::NV;
     __shared__ float p_lds[kWaves][2][4][kTT];
     __shared__ float o_lds[kWaves][4][D];
     __shared__ float m_lds[kWaves][4], l_lds[kWaves][4];
@@ -122,7 +300,10 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
     const int ch = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
     const int t0 = ch * kChunkM;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+    // the wave index is wave-uniform: say so, so that every per-wave
+    // quantity (token range, tile offsets) stays in scalar registers
+    const int tid = threadIdx.x, l = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = qpk;                                  // 1..4
     float *outs = out + ((int64_t)s * n_q + (int64_t)kvh * qpk) * D;
     if (t0 >= L) {
@@ -132,7 +313,7 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
         return;
     }
     const int wb = t0 + w * kTW;
-    const int we = min(L, wb + kTW);
+    const int n_tok = min(L, wb + kTW) - wb;            // may be <= 0
     const Planes K = planes_of(g, bt.base[s], layer, 0);
     const Planes V = planes_of(g, bt.base[s], layer, 1);
     const int64_t hbase = (int64_t)kvh * g.gph;
@@ -144,18 +325,21 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
     float qv[GPD][16];
     float amax = 0.0f;
-    double qsum[GPD];
+    float qsum[GPD];
 #pragma unroll
     for (int gg = 0; gg < GPD; gg++) {
-        qsum[gg] = 0.0;
+        double sum = 0.0;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const int dim = 64 * gg + (j < 8 ? 8 * qq + j : 32 + 8 * qq + j - 8);
             const float v = ha < G ? qs[ha * D + dim] : 0.0f;
             qv[gg][j] = v;
             amax = fmaxf(amax, fabsf(v));
-            qsum[gg] += (double)v;
+            sum += (double)v;
         }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        qsum[gg] = (float)sum;
     }
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
@@ -172,110 +356,65 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
             wd[j >> 2] |= (uint32_t)(digit_of(z, pa) & 0xff) << (8 * (j & 3));
         }
         A[gg] = v4i{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
-        qsum[gg] += __shfl_xor(qsum[gg], 16, 64);
-        qsum[gg] += __shfl_xor(qsum[gg], 32, 64);
     }
     // constants of the head whose scores this lane receives (ho = l/16)
     const int ho = l >> 4, tl = l & 15;
     const int esh_o = __shfl(esh, 4 * ho, 64);
-    const double cs = (double)rs * ldexp(1.0, -esh_o);
-    double bq[GPD];
+    float wsc[4];
 #pragma unroll
-    for (int gg = 0; gg < GPD; gg++) bq[gg] = (double)rs * __shfl(qsum[gg], 4 * ho, 64);
+    for (int p = 0; p < 4; p++) wsc[p] = ldexpf(rs, 24 - 8 * p - esh_o);
+    float bq[GPD];
+#pragma unroll
+    for (int gg = 0; gg < GPD; gg++) bq[gg] = rs * __shfl(qsum[gg], 4 * ho, 64);
 
     // V lane roles: l = grp*4*TS + ts*4 + x; block (grp, ts) = token slot ts
     // of group grp, x = head (A row) and dim column (B).  Column x of
     // accumulator m is dim 64grp + 32(m>=8) + 8x + m%8.
     const int x = l & 3, ts = (l >> 2) % TS, grp = (l >> 2) / TS;
 
-    v4f acc[16];
-#pragma unroll
-    for (int m = 0; m < 16; m++) acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    float bacc = 0.0f, lsum = 0.0f;
-    float mrun[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    LaneOffs P;
+    {
+        const int64_t wbytes = g.max_groups * 32, sbytes = g.max_groups * 4;
+        P.kw = plane_rsrc(K.w, wbytes); P.ks = plane_rsrc(K.s, sbytes);
+        P.kb = plane_rsrc(K.b, sbytes); P.vw = plane_rsrc(V.w, wbytes);
+        P.vs = plane_rsrc(V.s, sbytes); P.vb = plane_rsrc(V.b, sbytes);
+        const int64_t gk = hbase + (int64_t)(wb + tl) * GPD;
+        const int64_t gv = hbase + (int64_t)(wb + ts) * GPD + grp;
+        P.kwo = (uint32_t)(gk * 32 + qq * 8);
+        P.kso = (uint32_t)(gk * 4);
+        P.vwo = (uint32_t)(gv * 32 + x * 8);
+        P.vso = (uint32_t)(gv * 4);
+    }
 
-    Tile<D> cur, nxt;
-    if (wb < we) load_tile<D>(cur, K, V, hbase, wb, we, tl, qq, ts, grp, x);
-    int buf = 0;
-    for (int t = wb; t < we; t += kTT) {
-        if (t + kTT < we) load_tile<D>(nxt, K, V, hbase, t + kTT, we, tl, qq, ts, grp, x);
+    WaveState<D> S;
+#pragma unroll
+    for (int m = 0; m < 16; m++) S.acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    S.bacc = 0.0f;
+    S.lsum = 0.0f;
+    S.m0 = S.m1 = S.m2 = S.m3 = -INFINITY;
 
-        // ---- K: scores of this lane's head ho for tokens t + 16k + tl
-        float sc[NK];
-        float mt = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < NK; k++) {
-            double a = 0.0;
-#pragma unroll
-            for (int gg = 0; gg < GPD; gg++) {
-                const uint2 raw = cur.kw[k][gg];
-                const v4i B = v4i{(int)(raw.x & 0x0F0F0F0Fu), (int)(raw.y & 0x0F0F0F0Fu),
-                                  (int)((raw.x >> 4) & 0x0F0F0F0Fu),
-                                  (int)((raw.y >> 4) & 0x0F0F0F0Fu)};
-                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[gg], B,
-                                                                    v4i{0, 0, 0, 0}, 0, 0, 0);
-                const double dot = ((double)d[0] * 16777216.0 + (double)d[1] * 65536.0) +
-                                   ((double)d[2] * 256.0 + (double)d[3]);
-                a += cs * ((double)cur.ks[k][gg] * dot) + (double)cur.kb[k][gg] * bq[gg];
-            }
-            sc[k] = t + 16 * k + tl < we ? (float)a : -INFINITY;
-            mt = fmaxf(mt, sc[k]);
+    // two tiles in flight per wave, ping-pong registers.  The barrier keeps
+    // the scheduler from sinking a prefetch down to its use.
+    Tile<D> ta, tb;
+    auto load = [&](Tile<D> &T, int dt) {
+        load_tile<D>(T, P, dt);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto proc = [&](const Tile<D> &T, int dt, float (*pl)[kTT]) {
+        process_tile<D>(S, T, dt, n_tok, A, wsc, bq, pl, G, ho, tl, ts, x);
+    };
+    // Prefetches are unconditional so that every wait in the loop counts the
+    // same number of younger loads; past the end they re-read the last tile.
+    if (n_tok > 0) {
+        const int last = ((n_tok - 1) / kTT) * kTT;
+        load(ta, 0);
+        for (int dt = 0; dt < n_tok; dt += 2 * kTT) {
+            load(tb, min(dt + kTT, last));
+            proc(ta, dt, p_lds[w][0]);
+            if (dt + kTT >= n_tok) break;
+            load(ta, min(dt + 2 * kTT, last));
+            proc(tb, dt + kTT, p_lds[w][1]);
         }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, 64));
-
-        // ---- lazy rescale: move the running max only when a head's tile max
-        // exceeds it by more than kTau, so p = exp(s - mrun) stays <= e^kTau
-        float mth[4];
-        bool up = false;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            mth[r] = __shfl(mt, 16 * r, 64);
-            up |= mth[r] > mrun[r] + kTau;
-        }
-        if (up) {
-            float f[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float mn = mth[r] > mrun[r] + kTau ? mth[r] : mrun[r];
-                f[r] = exp2f((mrun[r] - mn) * EAKV_LOG2E);
-                mrun[r] = mn;
-            }
-#pragma unroll
-            for (int m = 0; m < 16; m++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[m][r] *= f[r];
-            const float fx = x == 0 ? f[0] : (x == 1 ? f[1] : (x == 2 ? f[2] : f[3]));
-            bacc *= fx;
-            lsum *= fx;
-        }
-        const float mho = ho == 0 ? mrun[0] : (ho == 1 ? mrun[1] : (ho == 2 ? mrun[2] : mrun[3]));
-#pragma unroll
-        for (int k = 0; k < NK; k++)
-            p_lds[w][buf][ho][16 * k + tl] = exp2f((sc[k] - mho) * EAKV_LOG2E);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- V: p*scale rows x 4 dims columns per 4x4x1 block
-#pragma unroll
-        for (int j = 0; j < NV; j++) {
-            const float p = x < G ? p_lds[w][buf][x][TS * j + ts] : 0.0f;
-            const float a = p * cur.vs[j];
-            bacc = fmaf(p, cur.vb[j], bacc);
-            lsum += grp == 0 ? p : 0.0f;
-            const uint2 raw = cur.vw[j];
-            const uint32_t lo0 = raw.x & 0x0F0F0F0Fu, lo1 = raw.y & 0x0F0F0F0Fu;
-            const uint32_t hi0 = (raw.x >> 4) & 0x0F0F0F0Fu, hi1 = (raw.y >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int m = 0; m < 16; m++) {
-                const uint32_t wd = m < 8 ? (m < 4 ? lo0 : lo1) : (m < 12 ? hi0 : hi1);
-                const float nb = (float)((wd >> (8 * (m & 3))) & 0xffu);
-                acc[m] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, nb, acc[m], 0, 0, 0);
-            }
-        }
-        cur = nxt;
-        buf ^= 1;
     }
 
     // sum the token slots (lane bits 2 .. 2+log2(TS)-1)
@@ -284,24 +423,26 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
 #pragma unroll
         for (int m = 0; m < 16; m++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[m][r] += __shfl_xor(acc[m][r], o, 64);
-        bacc += __shfl_xor(bacc, o, 64);
-        lsum += __shfl_xor(lsum, o, 64);
+            for (int r = 0; r < 4; r++) S.acc[m][r] += __shfl_xor(S.acc[m][r], o, 64);
+        S.bacc += __shfl_xor(S.bacc, o, 64);
     }
+    // lsum lives in the score layout: head ho, summed over its 16 token lanes
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) S.lsum += __shfl_xor(S.lsum, o, 64);
     float bsum[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) bsum[r] = __shfl(bacc, grp * 4 * TS + r, 64);
+    for (int r = 0; r < 4; r++) bsum[r] = __shfl(S.bacc, grp * 4 * TS + r, 64);
     if (ts == 0) {
 #pragma unroll
         for (int m = 0; m < 16; m++) {
             const int dim = 64 * grp + (m >= 8 ? 32 : 0) + 8 * x + (m & 7);
 #pragma unroll
-            for (int r = 0; r < 4; r++) o_lds[w][r][dim] = acc[m][r] + bsum[r];
+            for (int r = 0; r < 4; r++) o_lds[w][r][dim] = S.acc[m][r] + bsum[r];
         }
     }
-    if (l < 4) {
-        m_lds[w][l] = mrun[l];
-        l_lds[w][l] = lsum;
+    if ((l & 15) == 0) {
+        m_lds[w][l >> 4] = sel4(l >> 4, S.m0, S.m1, S.m2, S.m3);
+        l_lds[w][l >> 4] = S.lsum;
     }
     __syncthreads();
 
