@@ -231,6 +231,31 @@ def cpu_baseline(cfg, budget_s=12.0):
     }
 
 
+def copy_calibration(n_bytes, reps=5):
+    """Copy n_bytes device-to-device `reps` times with the synth library's
+    streaming copy kernel; prints the bytes read and written per launch."""
+    from eakv_amd import hipmem as H
+    lib = Synth().lib
+    lib.eakv_synth_copy.restype = C.c_int
+    lib.eakv_synth_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
+    src = H.DeviceArray((n_bytes // 4,))
+    dst = H.DeviceArray((n_bytes // 4,))
+    e0, e1 = H.Event(), H.Event()
+    ms = []
+    for _ in range(reps):
+        e0.record(None)
+        rc = lib.eakv_synth_copy(dst.ptr, src.ptr, n_bytes, None)
+        if rc:
+            raise RuntimeError(f"copy launch failed: {rc}")
+        e1.record(None)
+        e1.synchronize()
+        ms.append(e0.elapsed_ms(e1))
+    print(json.dumps({"copy_bytes_read": n_bytes, "copy_bytes_written": n_bytes,
+                      "launches": reps, "ms": [round(m, 4) for m in ms],
+                      "gbs_read_plus_write": round(2 * n_bytes / min(ms) / 1e6, 1)}),
+          flush=True)
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -249,11 +274,17 @@ def main():
     ap.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
     ap.add_argument("--ctx", type=int, default=None, help="override context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB, 5 times (the "
+                         "known-size kernel for HBM byte counters), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
               "sharding across GPUs is not built in this version", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration << 20)
+        return
 
     from eakv_amd import hipmem as H
     log = lambda *a: print(*a, file=sys.stderr, flush=True)

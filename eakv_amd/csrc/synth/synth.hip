@@ -75,3 +75,33 @@ extern "C" int eakv_synth_fill(float *out, int64_t n_rows, int64_t n_tok, int d,
                        (hipStream_t)stream, out, n, n_tok, d, *p);
     return (int)hipGetLastError();
 }
+
+namespace {
+
+// Plain streaming copy, 16 B per lane per iteration: the known-size kernel
+// that HBM byte counters (FETCH_SIZE, WRITE_SIZE) are calibrated against.
+__global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst,
+                                                   const uint4 *__restrict__ src,
+                                                   int64_t n16)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16;
+         i += (int64_t)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+}  // namespace
+
+// dst[0, n_bytes) = src[0, n_bytes); n_bytes a multiple of 16, both 16-aligned.
+extern "C" int eakv_synth_copy(void *dst, const void *src, int64_t n_bytes,
+                               void *stream)
+{
+    if (n_bytes <= 0) return 0;
+    if ((n_bytes & 15) || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15))
+        return (int)hipErrorInvalidValue;
+    const int64_t n16 = n_bytes / 16;
+    int64_t blocks = (n16 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (uint4 *)dst, (const uint4 *)src, n16);
+    return (int)hipGetLastError();
+}
