@@ -13,17 +13,23 @@
 //
 // Two block programs:
 //
-// mfma_kernel (groups of up to 4 q heads per kv head): 4 waves x 512 tokens.
-//   K phase, 16 tokens per step: one v_mfma_i32_16x16x64_i8 per 64-dim group.
+// mfma_kernel (up to 4 q heads per kv head): 4 waves x 1024 tokens per block.
+//   Each wave walks its tokens in 32-token tiles, two tiles in flight
+//   (ping-pong registers, buffer loads issued one tile ahead).  Per tile:
+//   K, 16 tokens per v_mfma_i32_16x16x64_i8 and 64-dim group:
 //     A = the q heads as 32-bit fixed point split into four signed bytes
 //         (rows 4h+p: head h, byte p), B = the token's nibbles as int8 (the
-//         packed bytes masked, no conversion).  The exact integer dots are
-//         recombined in f64 and  score = (s0*dot0 + s1*dot1)/sqrt(d)
-//         + (b0*sum q0 + b1*sum q1)/sqrt(d), rounded once to f32.
-//   V phase, 8 (d=128) or 16 (d=64) tokens per step:
-//     v_mfma_f32_4x4x1f32 outer products: block (group, token slot), rows =
-//     4 heads with A = p*scale, columns = 4 dims with B = nibble; the bias
-//     enters as sum p*bias per (head, group).  p = exp(score - chunk max).
+//         packed bytes masked, no conversion).  The exact integer dot of each
+//         byte row is recombined in f32 with weights 2^24, 2^16, 2^8, 1
+//         (times 2^-e/sqrt(d)), and score = s*dot + b*sum(q)/sqrt(d).
+//   Online softmax with a lazy running max: the running max of a head moves
+//     only when a tile max exceeds it by more than kTau, so every
+//     p = exp(score - max) stays <= e^kTau and the accumulators are rescaled
+//     rarely.
+//   V, v_mfma_f32_4x4x1f32 outer products: block (group, token slot), rows =
+//     4 heads with A = p*scale, columns = 4 dims with B = nibble as float;
+//     the bias enters as sum p*bias per (head, group).  p moves from the score
+//     layout (lane = head x token) to the V layout through LDS.
 //   Waves are merged in LDS, then chunks across blocks.
 // valu_kernel (wider groups): one lane per token for K with the reference
 //   arithmetic, then V by dims; same partial/merge scheme.
@@ -699,7 +705,9 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
     const float rs = 1.0f / sqrtf((float)g->head_dim);
     float *part = (float *)work;
     const int ml = max_len(b);
-    if (qpk <= 4) {
+    // the MFMA program addresses a plane with 32-bit buffer offsets
+    const bool small_planes = g->max_groups * 32 <= (int64_t)0x7fffffff;
+    if (qpk <= 4 && small_planes) {
         const int mc = ml > 0 ? (ml + kChunkM - 1) / kChunkM : 1;
         const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
         if (g->head_dim == 64)
