@@ -156,8 +156,7 @@ static int fused_launch(eakv_cache_t *const *caches, int n, int layer,
     }
     const size_t need = eakvd_fused_work_bytes(&c0->geom, &b, n_q);
     return eakvd_fused(&c0->geom, &b, layer, d_q, n_q, n_kv, d_out,
-                       (char *)c0->work + (c0->work_bytes - need), c0->counters,
-                       stream);
+                       (char *)c0->work + (c0->work_bytes - need), stream);
 }
 
 int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,

@@ -129,21 +129,14 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
     if (e) goto hip_fail;
     e = eakvd_malloc((void **)&c->dev, c->dev_bytes);
     if (e) goto hip_fail;
-    e = eakvd_malloc((void **)&c->counters,
-                     EAKVD_COUNTERS(n_kv_heads) * sizeof(unsigned));
-    if (e) goto hip_fail;
     /* the reference calloc()s its planes (cache.c:33) */
     e = eakvd_memset_async(c->dev, 0, c->dev_bytes, c->stream);
-    if (!e) e = eakvd_memset_async(c->counters, 0,
-                                   EAKVD_COUNTERS(n_kv_heads) * sizeof(unsigned),
-                                   c->stream);
     if (!e) e = eakvd_stream_sync(c->stream);
     if (e) goto hip_fail;
     return c;
 
 hip_fail:
     eakvi_hip_fail(e, "cache_create");
-    if (c->counters) eakvd_free(c->counters);
     if (c->dev) eakvd_free(c->dev);
     if (c->stream) eakvd_stream_destroy(c->stream);
     free(c);
@@ -157,7 +150,6 @@ void eakv_cache_free(eakv_cache_t *c)
     int ok = eakvi_enter(c, &prev) == EAKV_OK;
     if (c->stream) eakvd_stream_sync(c->stream);
     if (c->work) eakvd_free(c->work);
-    if (c->counters) eakvd_free(c->counters);
     if (c->dev) eakvd_free(c->dev);
     if (c->stream) eakvd_stream_destroy(c->stream);
     if (ok) eakvi_leave(prev);

@@ -103,13 +103,11 @@ typedef struct {
 
 size_t eakvd_fused_work_bytes(const eakvd_geom *g, const eakvd_batch *b,
                               int n_q);
-/* counters: EAKVD_MAX_BATCH*n_kv_heads u32, all zero on entry; the launch
- * leaves them zero again (the last block of each (sequence, kv head) resets
- * its own).  Launches that share a counter array must not overlap. */
-#define EAKVD_COUNTERS(n_kv_heads) ((size_t)EAKVD_MAX_BATCH * (n_kv_heads))
+/* work: eakvd_fused_work_bytes() of device scratch for the per-chunk
+ * partial results; launches that share it must not overlap. */
 int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
                 const float *q, int n_q, int n_kv, float *out, void *work,
-                unsigned *counters, void *stream);
+                void *stream);
 
 #ifdef __cplusplus
 }

@@ -14,18 +14,20 @@
 // Two block programs:
 //
 // mfma_kernel (up to 4 q heads per kv head): 4 waves x 1024 tokens per block.
-//   Each wave walks its tokens in 32-token tiles, two tiles in flight
-//   (ping-pong registers, buffer loads issued one tile ahead).  Per tile:
+//   Each wave walks its tokens in 32-token tiles, two pipeline stages in
+//   flight (ping-pong registers, buffer loads issued one stage ahead):
 //   K, 16 tokens per v_mfma_i32_16x16x64_i8 and 64-dim group:
 //     A = the q heads as 32-bit fixed point split into four signed bytes
 //         (rows 4h+p: head h, byte p), B = the token's nibbles as int8 (the
 //         packed bytes masked, no conversion).  The exact integer dot of each
 //         byte row is recombined in f32 with weights 2^24, 2^16, 2^8, 1
 //         (times 2^-e/sqrt(d)), and score = s*dot + b*sum(q)/sqrt(d).
-//   Online softmax with a lazy running max: the running max of a head moves
-//     only when a tile max exceeds it by more than kTau, so every
-//     p = exp(score - max) stays <= e^kTau and the accumulators are rescaled
-//     rarely.
+//   Online softmax in the log2 domain with a lazy running max: the running
+//     max of a head moves only when a tile max exceeds it by more than kTau,
+//     so every p = 2^(score - max) stays <= 2^kTau and the accumulators are
+//     rescaled rarely.
+//   The pipeline runs V(i) beside K(i+1): the K loads of a tile are issued
+//     one tile ahead of its V loads.
 //   V, v_mfma_f32_4x4x1f32 outer products: block (group, token slot), rows =
 //     4 heads with A = p*scale, columns = 4 dims with B = nibble as float;
 //     the bias enters as sum p*bias per (head, group).  p moves from the score
@@ -40,13 +42,12 @@ namespace {
 // ------------------------------------------------------------------ MFMA
 
 constexpr int kWaves = 4;
-constexpr int kTW = 1024;               // tokens per wave per chunk
-constexpr int kChunkM = kWaves * kTW;   // tokens per block
-#ifndef EAKV_FUSED_TT
-#define EAKV_FUSED_TT 32
+constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
+#ifndef EAKV_FUSED_BLOCKS_PER_CU
+#define EAKV_FUSED_BLOCKS_PER_CU 3
 #endif
-constexpr int kTT = EAKV_FUSED_TT;      // tokens per tile (one pipeline stage)
-constexpr float kTau = 8.0f;            // lazy-rescale headroom, e^8
+constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
+constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
 
 __device__ __forceinline__ int sext8(int v) { return (int)(int8_t)(v & 0xff); }
 
@@ -63,19 +64,28 @@ __device__ __forceinline__ int digit_of(int z, int p)
     return p == 0 ? d3 : (p == 1 ? d2 : (p == 2 ? d1 : d0));
 }
 
-// One lane's share of a kTT-token tile: the packed K bytes and K scale/bias
-// of its MFMA sub-tiles, and the packed V bytes and V scale/bias of its
-// V steps.
+// Tile geometry.  K: 16-token sub-tiles (one int8 MFMA per 64-dim group).
+// V: a token's packed bytes of one kv head are DW = D/8 dwords; in the V
+// layout lane l holds dword u = l % DW of token slot T = l / DW, so one V
+// step covers TSV = 64/DW tokens (4 at d=128, 8 at d=64).
 template <int D>
-struct Tile {
+struct Geo {
     static constexpr int GPD = D / 64;
-    static constexpr int NK = kTT / 16;          // K sub-tiles of 16 tokens
-    static constexpr int TS = 16 / GPD;          // V token slots per step
-    static constexpr int NV = kTT / TS;          // V steps
+    static constexpr int DW = D / 8;
+    static constexpr int TSV = 64 / DW;
+    static constexpr int NV = kTT / TSV;       // V steps per tile
+    static constexpr int NK = kTT / 16;        // K sub-tiles per tile
+};
+
+// One lane's share of a pipeline stage: the K bytes, K scale/bias and V
+// scale/bias of one tile (score layout: token 16k + tl), and the packed V
+// dwords of the tile before it (V layout).
+template <int D>
+struct Stage {
+    static constexpr int GPD = Geo<D>::GPD, NK = Geo<D>::NK, NV = Geo<D>::NV;
     uint2 kw[NK][GPD];
-    float ks[NK][GPD], kb[NK][GPD];
-    uint2 vw[NV];
-    float vs[NV], vb[NV];
+    float ks[NK][GPD], kb[NK][GPD], vs[NK][GPD], vb[NK][GPD];
+    uint32_t vw[NV];
 };
 
 // Buffer resources of the six planes (scalar registers) and this lane's byte
@@ -84,7 +94,7 @@ struct Tile {
 // no per-lane address arithmetic.  Reads past a plane's end return 0.
 struct LaneOffs {
     __amdgpu_buffer_rsrc_t kw, vw, ks, kb, vs, vb;
-    uint32_t kwo, kso, vwo, vso;
+    uint32_t kwo, so, vwo;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void *p, int64_t bytes)
@@ -100,64 +110,65 @@ __device__ __forceinline__ uint2 ldb64(__amdgpu_buffer_rsrc_t r, uint32_t vo, ui
     return uint2{v[0], v[1]};
 }
 
-__device__ __forceinline__ float ldf(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so)
+__device__ __forceinline__ uint32_t ldb32(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so)
 {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0));
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0);
 }
 
-// The tile at token offset dt of the wave.  A tile can run up to kTT - 1
-// tokens past the wave's last token; those reads stay inside the plane (or
-// return 0 beyond it) and their scores are masked to -inf, so their weight is
-// exactly 0.
+// Loads of the tile at token offset dt of the wave.  A tile can run up to
+// kTT - 1 tokens past the wave's last token; those reads stay inside the
+// plane (or return 0 beyond it), their scores are masked to -inf and their
+// weight is exactly 0.  dt is the same in every lane; readfirstlane makes
+// that visible, so the tile offset goes to the scalar soffset operand.
 template <int D>
-__device__ __forceinline__ void load_tile(Tile<D> &T, const LaneOffs &P, int dt)
+__device__ __forceinline__ void load_k(Stage<D> &T, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
-    constexpr int TS = Tile<D>::TS;
-    // dt is the same in every lane; readfirstlane makes that visible, so the
-    // tile offsets go to the scalar soffset operand
     const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
     const uint32_t ws = du * GPD * 32, ss = du * GPD * 4;
 #pragma unroll
-    for (int k = 0; k < Tile<D>::NK; k++) {
+    for (int k = 0; k < Geo<D>::NK; k++) {
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
             T.kw[k][gg] = ldb64(P.kw, P.kwo + (16 * k * GPD + gg) * 32, ws);
+        const uint32_t o = P.so + 16 * k * GPD * 4;
         if (GPD == 2) {
-            const uint2 sv = ldb64(P.ks, P.kso + 16 * k * GPD * 4, ss);
-            const uint2 bv = ldb64(P.kb, P.kso + 16 * k * GPD * 4, ss);
-            T.ks[k][0] = __uint_as_float(sv.x); T.ks[k][GPD - 1] = __uint_as_float(sv.y);
-            T.kb[k][0] = __uint_as_float(bv.x); T.kb[k][GPD - 1] = __uint_as_float(bv.y);
+            const uint2 a = ldb64(P.ks, o, ss), b = ldb64(P.kb, o, ss);
+            const uint2 c = ldb64(P.vs, o, ss), d = ldb64(P.vb, o, ss);
+            T.ks[k][0] = __uint_as_float(a.x); T.ks[k][GPD - 1] = __uint_as_float(a.y);
+            T.kb[k][0] = __uint_as_float(b.x); T.kb[k][GPD - 1] = __uint_as_float(b.y);
+            T.vs[k][0] = __uint_as_float(c.x); T.vs[k][GPD - 1] = __uint_as_float(c.y);
+            T.vb[k][0] = __uint_as_float(d.x); T.vb[k][GPD - 1] = __uint_as_float(d.y);
         } else {
-            T.ks[k][0] = ldf(P.ks, P.kso + 16 * k * 4, ss);
-            T.kb[k][0] = ldf(P.kb, P.kso + 16 * k * 4, ss);
+            T.ks[k][0] = __uint_as_float(ldb32(P.ks, o, ss));
+            T.kb[k][0] = __uint_as_float(ldb32(P.kb, o, ss));
+            T.vs[k][0] = __uint_as_float(ldb32(P.vs, o, ss));
+            T.vb[k][0] = __uint_as_float(ldb32(P.vb, o, ss));
         }
     }
-#pragma unroll
-    for (int j = 0; j < Tile<D>::NV; j++) {
-        T.vw[j] = ldb64(P.vw, P.vwo + TS * j * GPD * 32, ws);
-        T.vs[j] = ldf(P.vs, P.vso + TS * j * GPD * 4, ss);
-        T.vb[j] = ldf(P.vb, P.vso + TS * j * GPD * 4, ss);
-    }
 }
 
-// State carried across the tiles of one wave.  The running maxima are
-// wave-uniform scalars.
+template <int D>
+__device__ __forceinline__ void load_v(Stage<D> &T, const LaneOffs &P, int dt)
+{
+    constexpr int GPD = D / 64;
+    const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
+    const uint32_t ws = du * GPD * 32;
+#pragma unroll
+    for (int j = 0; j < Geo<D>::NV; j++)
+        T.vw[j] = ldb32(P.vw, P.vwo + Geo<D>::TSV * j * GPD * 32, ws);
+}
+
+// State carried across the tiles of one wave.  acc (V layout): lane (T, u)
+// holds, for nibble e of its dword, the partial output of heads r = 0..3.
+// Score layout (lane = head ho x token tl): the running max m of head ho,
+// the softmax denominator lsum and the bias sums sum p*bias per group.
 template <int D>
 struct WaveState {
-    v4f acc[16];
-    float bacc, lsum;
-    float m0, m1, m2, m3;
+    v4f acc[8];
+    float bacc[D / 64];
+    float lsum, m;
 };
-
-__device__ __forceinline__ float sel4(int i, float a, float b, float c, float d)
-{
-    float r = a;
-    r = i == 1 ? b : r;
-    r = i == 2 ? c : r;
-    r = i == 3 ? d : r;
-    return r;
-}
 
 // x & 0x0F0F0F0F hidden from the optimizer, so that extracting byte k of the
 // result stays one v_cvt_f32_ubyte<k>
@@ -175,6 +186,16 @@ __device__ __forceinline__ uint32_t nib_hi(uint32_t x)
     return r;
 }
 
+// p * v with 0 * anything = 0 (v_mul_legacy_f32; otherwise IEEE rounding).
+// A tile can cover tokens past the sequence end whose p is 0 but whose stale
+// scale or bias may be non-finite; their products must stay 0.
+__device__ __forceinline__ float mul_zero(float p, float v)
+{
+    float r;
+    asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(p), "v"(v));
+    return r;
+}
+
 __device__ __forceinline__ float row_max16(float v)
 {
     // max over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1)
@@ -185,141 +206,168 @@ __device__ __forceinline__ float row_max16(float v)
     return v;
 }
 
-template <int D>
-__device__ __forceinline__ void process_tile(
-    WaveState<D> &S, const Tile<D> &T, int dt, int n_tok, const v4i *A,
-    const float *wsc, const float *bq, float (*pl)[kTT], int G, int ho,
-    int tl, int ts, int x)
+// Slot of a = p*scale for (group g, head h, token tau of a tile) in a wave's
+// a buffer (GPD x 128 floats).  Written in the score layout, read in the V
+// layout; the swizzle keeps both free of LDS bank conflicts.
+__device__ __forceinline__ int a_slot(int g, int h, int tau)
 {
-    constexpr int GPD = D / 64;
-    constexpr int TS = Tile<D>::TS;
-    constexpr int NK = Tile<D>::NK;
-    constexpr int NV = Tile<D>::NV;
+    return g * 128 + ((tau * 4 + h) ^ (g * 16) ^ (((tau >> 3) & 1) * 2));
+}
 
-    // ---- K: per sub-tile, the digit-row dots of both groups, then their
-    // recombination: the exact integer dot of each digit row times its
-    // weight (wsc holds 2^24, 2^16, 2^8, 1 times 2^-e/sqrt(d)), in f32.
-    float sc[NK];
-    float mt = -INFINITY;
+// K of one tile: per 16-token sub-tile, the digit-row dots of each group on
+// the int8 matrix core (k_mfma), then their recombination (k_recomb).  The
+// four digit rows r (weights 2^24, 2^16, 2^8, 1) are paired exactly in int32,
+// H = 256*d0 + d1 and Lo = 256*d2 + d3 (|H|, |Lo| < 2^25), and
+// u = H*wh + Lo*wl with wh = 2^16*wl, wl = 2^-e*log2(e)/sqrt(d).  Scores are
+// in the log2 domain: sc = log2(e) * (q.k)/sqrt(d); masked tokens get -inf.
+template <int D>
+__device__ __forceinline__ void k_mfma(const Stage<D> &T, const v4i *A,
+                                       v4i (*dk)[D / 64])
+{
 #pragma unroll
-    for (int k = 0; k < NK; k++) {
-        v4i d[GPD];
+    for (int k = 0; k < Geo<D>::NK; k++)
 #pragma unroll
-        for (int gg = 0; gg < GPD; gg++) {
+        for (int gg = 0; gg < D / 64; gg++) {
             const uint2 raw = T.kw[k][gg];
             const v4i B = v4i{(int)nib_lo(raw.x), (int)nib_lo(raw.y), (int)nib_hi(raw.x),
                               (int)nib_hi(raw.y)};
-            d[gg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[gg], B, v4i{0, 0, 0, 0}, 0, 0, 0);
+            dk[k][gg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[gg], B, v4i{0, 0, 0, 0},
+                                                               0, 0, 0);
         }
-        float a = 0.0f;
-#pragma unroll
-        for (int gg = 0; gg < GPD; gg++) {
-            float u = (float)d[gg][3] * wsc[3];
-            u = fmaf((float)d[gg][2], wsc[2], u);
-            u = fmaf((float)d[gg][1], wsc[1], u);
-            u = fmaf((float)d[gg][0], wsc[0], u);
-            a = fmaf(T.ks[k][gg], u, fmaf(T.kb[k][gg], bq[gg], a));
-        }
-        sc[k] = dt + 16 * k + tl < n_tok ? a : -INFINITY;
-        mt = fmaxf(mt, sc[k]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    mt = row_max16(mt);
-
-    // ---- lazy rescale: move the running max only when a head's tile max
-    // exceeds it by more than kTau, so p = exp(s - mrun) stays <= e^kTau
-    const float t0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 0));
-    const float t1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 16));
-    const float t2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 32));
-    const float t3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mt), 48));
-    const bool u0 = t0 > S.m0 + kTau, u1 = t1 > S.m1 + kTau;
-    const bool u2 = t2 > S.m2 + kTau, u3 = t3 > S.m3 + kTau;
-    if (u0 || u1 || u2 || u3) {
-        const float n0 = u0 ? t0 : S.m0, n1 = u1 ? t1 : S.m1;
-        const float n2 = u2 ? t2 : S.m2, n3 = u3 ? t3 : S.m3;
-        const float f0 = exp2f((S.m0 - n0) * EAKV_LOG2E), f1 = exp2f((S.m1 - n1) * EAKV_LOG2E);
-        const float f2 = exp2f((S.m2 - n2) * EAKV_LOG2E), f3 = exp2f((S.m3 - n3) * EAKV_LOG2E);
-        S.m0 = n0; S.m1 = n1; S.m2 = n2; S.m3 = n3;
-#pragma unroll
-        for (int m = 0; m < 16; m++) {
-            S.acc[m][0] *= f0;
-            S.acc[m][1] *= f1;
-            S.acc[m][2] *= f2;
-            S.acc[m][3] *= f3;
-        }
-        S.bacc *= sel4(x, f0, f1, f2, f3);
-        S.lsum *= sel4(ho, f0, f1, f2, f3);
-    }
-    // p in the score layout (head ho, token 16k + tl); heads >= G get 0
-    const float mho = sel4(ho, S.m0, S.m1, S.m2, S.m3);
-#pragma unroll
-    for (int k = 0; k < NK; k++) {
-        const float p = ho < G ? exp2f((sc[k] - mho) * EAKV_LOG2E) : 0.0f;
-        S.lsum += p;
-        pl[ho][16 * k + tl] = p;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- V: rows p*scale (4 heads) x columns 4 dims per 4x4x1 block
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-        const float p = pl[x][TS * j + ts];
-        const float a = p * T.vs[j];
-        S.bacc = fmaf(p, T.vb[j], S.bacc);
-        const uint2 raw = T.vw[j];
-        // low nibbles (accumulators 0-7), then high nibbles (8-15)
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-            const uint32_t w0 = half ? nib_hi(raw.x) : nib_lo(raw.x);
-            const uint32_t w1 = half ? nib_hi(raw.y) : nib_lo(raw.y);
-            float nb[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                nb[e] = (float)(((e < 4 ? w0 : w1) >> (8 * (e & 3))) & 0xffu);
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                S.acc[8 * half + e] =
-                    __builtin_amdgcn_mfma_f32_4x4x1f32(a, nb[e], S.acc[8 * half + e], 0, 0, 0);
-        }
-        // keep the steps apart: hoisting later steps' conversions above these
-        // MFMAs only raises register pressure
-        __builtin_amdgcn_sched_barrier(0);
-    }
 }
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void mfma_kernel(
+__device__ __forceinline__ float k_recomb(const Stage<D> &T, const v4i *d, int k,
+                                          int dt, int n_tok, float wh, float wl,
+                                          const float *bq, int tl)
+{
+    float a = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < D / 64; gg++) {
+        const int hi = d[gg][0] * 256 + d[gg][1];
+        const int lo = d[gg][2] * 256 + d[gg][3];
+        const float u = fmaf((float)hi, wh, (float)lo * wl);
+        a = fmaf(T.ks[k][gg], u, fmaf(T.kb[k][gg], bq[gg], a));
+    }
+    return dt + 16 * k + tl < n_tok ? a : -INFINITY;
+}
+
+// Softmax weights of sub-tile k with the running max m of this lane's head:
+// p = 2^(sc - m) (0 for heads >= G), a = p*scale per group into the a
+// buffer, p*bias per group into bi.  Returns p.
+template <int D>
+__device__ __forceinline__ float p_write(const Stage<D> &T, int k, float sc, float m,
+                                         bool live, float *abuf, int ho, int tl,
+                                         float *bi)
+{
+    const float p = live ? __builtin_amdgcn_exp2f(sc - m) : 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < D / 64; gg++) {
+        abuf[a_slot(gg, ho, 16 * k + tl)] = mul_zero(p, T.vs[k][gg]);
+        bi[gg] += mul_zero(p, T.vb[k][gg]);
+    }
+    return p;
+}
+
+// The tile's softmax bookkeeping once the previous tile's V is accumulated.
+// Lazy rescale: a head's running max moves only when the tile's max exceeds
+// it by more than kTau (so p <= 2^kTau).  The common case (need false in
+// every lane) only adds the tile's sums; otherwise (rare: the first tile,
+// a new larger score) the moved maxima are set, the accumulators scaled by
+// 2^(old - new) and the tile's weights rewritten.
+template <int D>
+__device__ __forceinline__ void softmax_tail(
+    WaveState<D> &S, const Stage<D> &T, const float *sc, bool need, float psum,
+    float *bi, bool live, float *abuf, int ho, int tl)
+{
+    constexpr int NK = Geo<D>::NK, GPD = D / 64;
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        float mt = sc[0];
+#pragma unroll
+        for (int k = 1; k < NK; k++) mt = fmaxf(mt, sc[k]);
+        mt = row_max16(mt);
+        const float mn = live && mt > S.m + kTau ? mt : S.m;
+        const float f = live ? __builtin_amdgcn_exp2f(S.m - mn) : 1.0f;
+        S.m = mn;
+        psum = 0.0f;
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NK; k++) psum += p_write<D>(T, k, sc[k], S.m, live, abuf, ho, tl, bi);
+        S.lsum *= f;
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) S.bacc[gg] *= f;
+        const float f0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 0));
+        const float f1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 16));
+        const float f2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 32));
+        const float f3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 48));
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            S.acc[e][0] *= f0;
+            S.acc[e][1] *= f1;
+            S.acc[e][2] *= f2;
+            S.acc[e][3] *= f3;
+        }
+    }
+    S.lsum += psum;
+#pragma unroll
+    for (int gg = 0; gg < GPD; gg++) S.bacc[gg] += bi[gg];
+}
+
+// This lane's a of every V step of a tile (V layout: group of its dword,
+// head x = l%4, token TSV*j + T).  LDS accesses of one wave complete in
+// order, so the wavefront-scope fences cost no wait; they keep the compiler
+// from moving these reads above the writes of the tile.
+template <int D>
+__device__ __forceinline__ void read_a(const float *abuf, int gv, int x, int tv, float *ar)
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < Geo<D>::NV; j++) ar[j] = abuf[a_slot(gv, x, Geo<D>::TSV * j + tv)];
+}
+
+// One V step of a tile: 8 outer-product MFMAs (one per nibble of this lane's
+// dword), rows a = p*scale of the 4 heads, columns the nibbles as f32.
+template <int D>
+__device__ __forceinline__ void v_step(WaveState<D> &S, const Stage<D> &T,
+                                       const float *ar, int j)
+{
+    const uint32_t lo = nib_lo(T.vw[j]), hi = nib_hi(T.vw[j]);
+    float nb[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) nb[e] = (float)(((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xffu);
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        S.acc[e] = __builtin_amdgcn_mfma_f32_4x4x1f32(ar[j], nb[e], S.acc[e], 0, 0, 0);
+}
+
+// tw tokens per wave (a multiple of kTT); a block's chunk is kWaves * tw.
+// Writes the chunk's partial (m, l, o[D]) per q head of its kv head;
+// merge_kernel combines the chunks.
+template <int D>
+__global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
-    int n_q, int qpk, int n_kv, int max_chunks, float rs,
-    float *__restrict__ part, unsigned *__restrict__ cnt,
-    float *__restrict__ out)
+    int n_q, int qpk, int max_chunks, int tw, float rs, float *__restrict__ part)
 {
     constexpr int GPD = D / 64;
-    constexpr int TS = Tile<D>::TS;
-    __shared__ float p_lds[kWaves][2][4][kTT];
+    constexpr int DW = Geo<D>::DW, NK = Geo<D>::NK, NV = Geo<D>::NV;
+    __shared__ float a_lds[kWaves][2][GPD * 128];
     __shared__ float o_lds[kWaves][4][D];
     __shared__ float m_lds[kWaves][4], l_lds[kWaves][4];
-    __shared__ int last_flag;
 
     const int ch = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
-    const int t0 = ch * kChunkM;
+    const int t0 = ch * kWaves * tw;
+    if (t0 >= L) return;            // past this sequence's end: no partial
     // the wave index is wave-uniform: say so, so that every per-wave
     // quantity (token range, tile offsets) stays in scalar registers
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = qpk;                                  // 1..4
-    float *outs = out + ((int64_t)s * n_q + (int64_t)kvh * qpk) * D;
-    if (t0 >= L) {
-        // an empty context gives 0 * (1/0) = NaN, as the reference
-        if (L == 0 && ch == 0)
-            for (int i = tid; i < G * D; i += 256) outs[i] = __builtin_nanf("");
-        return;
-    }
-    const int wb = t0 + w * kTW;
-    const int n_tok = min(L, wb + kTW) - wb;            // may be <= 0
+    const int wb = t0 + w * tw;
+    const int n_tok = min(L, wb + tw) - wb;             // may be <= 0
     const Planes K = planes_of(g, bt.base[s], layer, 0);
     const Planes V = planes_of(g, bt.base[s], layer, 1);
     const int64_t hbase = (int64_t)kvh * g.gph;
@@ -328,7 +376,10 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
     // ---- q -> A operands.  Lane l: row i = l%16 (head ha = i/4, digit
     // pa = i%4), k-block qq = l/16; k-slot j of group gg holds dim
     // 64gg + 8qq + j (j < 8, low nibbles) or 64gg + 32 + 8qq + (j-8).
+    // Rows of heads >= G are zero (their q is read from head 0 and dropped).
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
+    const bool qrow = ha < G;
+    const float *qh = qs + (qrow ? ha : 0) * D;
     float qv[GPD][16];
     float amax = 0.0f;
     float qsum[GPD];
@@ -338,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const int dim = 64 * gg + (j < 8 ? 8 * qq + j : 32 + 8 * qq + j - 8);
-            const float v = ha < G ? qs[ha * D + dim] : 0.0f;
+            const float v = qrow ? qh[dim] : 0.0f;
             qv[gg][j] = v;
             amax = fmaxf(amax, fabsf(v));
             sum += (double)v;
@@ -363,20 +414,20 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
         }
         A[gg] = v4i{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
     }
-    // constants of the head whose scores this lane receives (ho = l/16)
+    // score layout: this lane receives the scores of head ho for token tl
     const int ho = l >> 4, tl = l & 15;
+    const bool live = ho < G;
     const int esh_o = __shfl(esh, 4 * ho, 64);
-    float wsc[4];
-#pragma unroll
-    for (int p = 0; p < 4; p++) wsc[p] = ldexpf(rs, 24 - 8 * p - esh_o);
+    // scores are kept in the log2 domain (times log2(e))
+    const float rs2 = rs * EAKV_LOG2E;
+    const float wl = ldexpf(rs2, -esh_o), wh = ldexpf(rs2, 16 - esh_o);
     float bq[GPD];
 #pragma unroll
-    for (int gg = 0; gg < GPD; gg++) bq[gg] = rs * __shfl(qsum[gg], 4 * ho, 64);
+    for (int gg = 0; gg < GPD; gg++) bq[gg] = rs2 * __shfl(qsum[gg], 4 * ho, 64);
 
-    // V lane roles: l = grp*4*TS + ts*4 + x; block (grp, ts) = token slot ts
-    // of group grp, x = head (A row) and dim column (B).  Column x of
-    // accumulator m is dim 64grp + 32(m>=8) + 8x + m%8.
-    const int x = l & 3, ts = (l >> 2) % TS, grp = (l >> 2) / TS;
+    // V layout: lane l = (token slot tv, dword u); u is dword uw of group gv;
+    // x = l%4 is the head row (A) and the column (B) of its 4x4x1 block.
+    const int tv = l / DW, u = l % DW, gv = u / 8, uw = u % 8, x = l & 3;
 
     LaneOffs P;
     {
@@ -385,70 +436,139 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
         P.kb = plane_rsrc(K.b, sbytes); P.vw = plane_rsrc(V.w, wbytes);
         P.vs = plane_rsrc(V.s, sbytes); P.vb = plane_rsrc(V.b, sbytes);
         const int64_t gk = hbase + (int64_t)(wb + tl) * GPD;
-        const int64_t gv = hbase + (int64_t)(wb + ts) * GPD + grp;
+        const int64_t gvv = hbase + (int64_t)(wb + tv) * GPD + gv;
         P.kwo = (uint32_t)(gk * 32 + qq * 8);
-        P.kso = (uint32_t)(gk * 4);
-        P.vwo = (uint32_t)(gv * 32 + x * 8);
-        P.vso = (uint32_t)(gv * 4);
+        P.so = (uint32_t)(gk * 4);
+        P.vwo = (uint32_t)(gvv * 32 + uw * 4);
     }
 
     WaveState<D> S;
 #pragma unroll
-    for (int m = 0; m < 16; m++) S.acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    S.bacc = 0.0f;
+    for (int e = 0; e < 8; e++) S.acc[e] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int gg = 0; gg < GPD; gg++) S.bacc[gg] = 0.0f;
     S.lsum = 0.0f;
-    S.m0 = S.m1 = S.m2 = S.m3 = -INFINITY;
+    S.m = -INFINITY;
 
-    // two tiles in flight per wave, ping-pong registers.  The barrier keeps
-    // the scheduler from sinking a prefetch down to its use.
-    Tile<D> ta, tb;
-    auto load = [&](Tile<D> &T, int dt) {
-        load_tile<D>(T, P, dt);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto proc = [&](const Tile<D> &T, int dt, float (*pl)[kTT]) {
-        process_tile<D>(S, T, dt, n_tok, A, wsc, bq, pl, G, ho, tl, ts, x);
-    };
-    // Prefetches are unconditional so that every wait in the loop counts the
-    // same number of younger loads; past the end they re-read the last tile.
+    // Software pipeline over the wave's tiles.  Stage i holds the K (and V
+    // scale/bias) of tile i+1 and the V dwords of tile i; iteration i runs
+    // V(i) beside K(i+1) and its softmax weights.  Two stages are in flight
+    // (ping-pong registers); the next stage's loads are issued before the
+    // current one is consumed.  Loads are unconditional so that every wait
+    // counts the same number of younger loads; past the end they re-read
+    // the last tile, and K scores past the end are masked.
     if (n_tok > 0) {
         const int last = ((n_tok - 1) / kTT) * kTT;
-        load(ta, 0);
-        for (int dt = 0; dt < n_tok; dt += 2 * kTT) {
-            load(tb, min(dt + kTT, last));
-            proc(ta, dt, p_lds[w][0]);
+        float *ab0 = a_lds[w][0], *ab1 = a_lds[w][1];
+        Stage<D> sa, sb;
+        auto load_stage = [&](Stage<D> &T, int dt) {
+            load_k<D>(T, P, min(dt + kTT, last));
+            load_v<D>(T, P, min(dt, last));
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // One basic block holds V(i), K(i+1) and the common softmax step of
+        // tile i+1.  V runs in steps of 8 MFMAs; the K and softmax work is
+        // cut into pieces (recombination and weights per sub-tile, the
+        // rescale test) and one piece rides along each V step, so the VALU
+        // work of one fills the matrix-core time of the other.  The sched
+        // barriers fix the pieces' order; inside a step the scheduler
+        // interleaves freely.
+        auto iter = [&](const Stage<D> &T, int dt, const float *av, float *ak) {
+            constexpr int NP = 2 * NK + 1;
+            float ar[NV], sc[NK], bi[GPD], psum = 0.0f;
+            bool need = false;
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
+            v4i dk[NK][GPD];
+            read_a<D>(av, gv, x, tv, ar);
+            k_mfma<D>(T, A, dk);
+#pragma unroll
+            for (int h = 0; h < NV; h++) {
+                v_step<D>(S, T, ar, h);
+#pragma unroll
+                for (int piece = 0; piece < NP; piece++) {
+                    if (1 + piece * (NV - 1) / NP != h) continue;
+                    if (piece < NK) {
+                        sc[piece] = k_recomb<D>(T, dk[piece], piece, dt + kTT, n_tok, wh,
+                                                wl, bq, tl);
+                    } else if (piece < 2 * NK) {
+                        const int k = piece - NK;
+                        psum += p_write<D>(T, k, sc[k], S.m, live, ak, ho, tl, bi);
+                    } else {
+                        float mt = sc[0];
+#pragma unroll
+                        for (int k = 1; k < NK; k++) mt = fmaxf(mt, sc[k]);
+                        need = live && mt - S.m > kTau;
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            softmax_tail<D>(S, T, sc, need, psum, bi, live, ak, ho, tl);
+        };
+        load_k<D>(sa, P, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage(sb, 0);
+        {
+            float sc[NK], bi[GPD], psum = 0.0f;
+            v4i dk[NK][GPD];
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
+            k_mfma<D>(sa, A, dk);
+            float mt = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < NK; k++) {
+                sc[k] = k_recomb<D>(sa, dk[k], k, 0, n_tok, wh, wl, bq, tl);
+                mt = fmaxf(mt, sc[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < NK; k++) psum += p_write<D>(sa, k, sc[k], S.m, live, ab0, ho, tl, bi);
+            softmax_tail<D>(S, sa, sc, live && mt - S.m > kTau, psum, bi, live, ab0, ho, tl);
+        }
+        for (int dt = 0;; dt += 2 * kTT) {
+            load_stage(sa, dt + kTT);
+            iter(sb, dt, ab0, ab1);
             if (dt + kTT >= n_tok) break;
-            load(ta, min(dt + 2 * kTT, last));
-            proc(tb, dt + kTT, p_lds[w][1]);
+            load_stage(sb, dt + 2 * kTT);
+            iter(sa, dt + kTT, ab1, ab0);
+            if (dt + 2 * kTT >= n_tok) break;
         }
     }
 
-    // sum the token slots (lane bits 2 .. 2+log2(TS)-1)
+    // ---- wave epilogue.  acc: sum the token slots (lane bits of tv).
 #pragma unroll
-    for (int o = 4; o < 4 * TS; o <<= 1) {
+    for (int o = DW; o < 64; o <<= 1)
 #pragma unroll
-        for (int m = 0; m < 16; m++)
+        for (int e = 0; e < 8; e++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) S.acc[m][r] += __shfl_xor(S.acc[m][r], o, 64);
-        S.bacc += __shfl_xor(S.bacc, o, 64);
+            for (int r = 0; r < 4; r++) S.acc[e][r] += __shfl_xor(S.acc[e][r], o, 64);
+    // score layout: lsum and the bias sums over the 16 token lanes of a head
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) {
+        S.lsum += __shfl_xor(S.lsum, o, 64);
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) S.bacc[gg] += __shfl_xor(S.bacc[gg], o, 64);
     }
-    // lsum lives in the score layout: head ho, summed over its 16 token lanes
+    float bsum[4];                                  // head r, this lane's group gv
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) S.lsum += __shfl_xor(S.lsum, o, 64);
-    float bsum[4];
+    for (int r = 0; r < 4; r++) {
+        float b = __shfl(S.bacc[0], 16 * r, 64);
+        if (GPD == 2) {
+            const float b1 = __shfl(S.bacc[GPD - 1], 16 * r, 64);
+            b = gv ? b1 : b;
+        }
+        bsum[r] = b;
+    }
+    if (tv == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) bsum[r] = __shfl(S.bacc, grp * 4 * TS + r, 64);
-    if (ts == 0) {
+        for (int e = 0; e < 8; e++) {
+            const int dim = 64 * gv + (e < 4 ? 0 : 32) + 4 * uw + (e & 3);
 #pragma unroll
-        for (int m = 0; m < 16; m++) {
-            const int dim = 64 * grp + (m >= 8 ? 32 : 0) + 8 * x + (m & 7);
-#pragma unroll
-            for (int r = 0; r < 4; r++) o_lds[w][r][dim] = S.acc[m][r] + bsum[r];
+            for (int r = 0; r < 4; r++) o_lds[w][r][dim] = S.acc[e][r] + bsum[r];
         }
     }
-    if ((l & 15) == 0) {
-        m_lds[w][l >> 4] = sel4(l >> 4, S.m0, S.m1, S.m2, S.m3);
-        l_lds[w][l >> 4] = S.lsum;
+    if (tl == 0) {
+        m_lds[w][ho] = S.m;
+        l_lds[w][ho] = S.lsum;
     }
     __syncthreads();
 
@@ -461,7 +581,7 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
         float lt = 0.0f, ot = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < kWaves; ww++) {
-            const float f = exp2f((m_lds[ww][h] - M) * EAKV_LOG2E);
+            const float f = __builtin_amdgcn_exp2f(m_lds[ww][h] - M);
             lt = fmaf(l_lds[ww][h], f, lt);
             ot = fmaf(o_lds[ww][h][dim], f, ot);
         }
@@ -472,34 +592,34 @@ __global__ __launch_bounds__(256, 2) void mfma_kernel(
             dst[1] = lt;
         }
     }
-
-    // ---- the last chunk of this (sequence, kv head) merges all chunks
-    __syncthreads();
-    const int n_chunks = (L + kChunkM - 1) / kChunkM;
-    unsigned *c = cnt + s * n_kv + kvh;
-    if (tid == 0) {
-        __threadfence();
-        last_flag = atomicAdd(c, 1u) == (unsigned)(n_chunks - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    for (int i = tid; i < G * D; i += 256) {
-        const int h = i / D, dim = i % D;
-        const float *p = part + ((int64_t)s * n_q + kvh * qpk + h) * max_chunks * (D + 2);
-        float M = 0.0f - 1000000.0f;
-        for (int cc = 0; cc < n_chunks; cc++) M = fmaxf(M, p[cc * (D + 2)]);
-        float lt = 0.0f, ot = 0.0f;
-        for (int cc = 0; cc < n_chunks; cc++) {
-            const float *pc = p + cc * (D + 2);
-            const float f = expf(pc[0] - M);
-            lt = fmaf(pc[1], f, lt);
-            ot = fmaf(pc[2 + dim], f, ot);
-        }
-        outs[i] = ot * (1.0f / lt);
-    }
-    if (tid == 0) *c = 0u;
 }
+
+// Merge of the MFMA program's chunk partials (log2 domain) per (q head,
+// sequence), in chunk order: M = max(-1e6 log2(e), m_c) (the reference's
+// max starts at -1e6), l = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M),
+// out = o * (1/l).  An empty sequence has no chunks: 0 * (1/0) = NaN, as the
+// reference.
+template <int D>
+__global__ __launch_bounds__(D) void merge_kernel(
+    eakvd_batch bt, int n_q, int max_chunks, int chunk,
+    const float *__restrict__ part, float *__restrict__ out)
+{
+    const int qh = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
+    const int n_chunks = (bt.seq_len[s] + chunk - 1) / chunk;
+    const float *p = part + ((int64_t)s * n_q + qh) * max_chunks * (D + 2);
+    float M = -1000000.0f * EAKV_LOG2E;
+    for (int c = 0; c < n_chunks; c++) M = fmaxf(M, p[c * (D + 2)]);
+    float lt = 0.0f, ot = 0.0f;
+#pragma unroll 4
+    for (int c = 0; c < n_chunks; c++) {
+        const float *pc = p + c * (D + 2);
+        const float f = __builtin_amdgcn_exp2f(pc[0] - M);
+        lt = fmaf(pc[1], f, lt);
+        ot = fmaf(pc[2 + i], f, ot);
+    }
+    out[((int64_t)s * n_q + qh) * D + i] = ot * (1.0f / lt);
+}
+
 
 // ------------------------------------------------------------------ VALU
 
@@ -678,6 +798,30 @@ __global__ __launch_bounds__(D) void combine_kernel(
     out[((int64_t)s * n_q + qh) * D + i] = __fmul_rn(o, 1.0f / l);
 }
 
+// Tokens per wave of the MFMA program: enough chunks per (sequence, kv
+// head) that the grid fills every CU with kBlocksPerCU resident blocks once
+// (a second partial round of blocks would idle most of the chip), at least
+// 128 tokens per wave (so chunks are no finer than the workspace allows) and
+// a multiple of the tile.
+int mfma_tokens_per_wave(int ml, int units)
+{
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                hipSuccess && v > 0)
+            n_cu = v;
+        else
+            n_cu = 256;
+    }
+    const int slots = n_cu * kBlocksPerCU;
+    const int per_unit = units >= slots ? 1 : slots / units;
+    int tw = (ml + per_unit * kWaves - 1) / (per_unit * kWaves);
+    tw = (tw + kTT - 1) / kTT * kTT;
+    return tw < 128 ? 128 : tw;
+}
+
 int max_len(const eakvd_batch *b)
 {
     int mx = 0;
@@ -697,8 +841,7 @@ extern "C" size_t eakvd_fused_work_bytes(const eakvd_geom *g,
 
 extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
                            int layer, const float *q, int n_q, int n_kv,
-                           float *out, void *work, unsigned *counters,
-                           void *stream)
+                           float *out, void *work, void *stream)
 {
     const hipStream_t st = (hipStream_t)stream;
     const int qpk = n_q / n_kv;
@@ -708,14 +851,22 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
     // the MFMA program addresses a plane with 32-bit buffer offsets
     const bool small_planes = g->max_groups * 32 <= (int64_t)0x7fffffff;
     if (qpk <= 4 && small_planes) {
-        const int mc = ml > 0 ? (ml + kChunkM - 1) / kChunkM : 1;
+        const int tw = mfma_tokens_per_wave(ml, b->n_seq * n_kv);
+        const int chunk = kWaves * tw;
+        const int mc = ml > 0 ? (ml + chunk - 1) / chunk : 1;
         const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
-        if (g->head_dim == 64)
+        const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
+        if (g->head_dim == 64) {
             hipLaunchKernelGGL(mfma_kernel<64>, grid, dim3(256), 0, st, *g, *b, layer,
-                               q, n_q, qpk, n_kv, mc, rs, part, counters, out);
-        else
+                               q, n_q, qpk, mc, tw, rs, part);
+            hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc,
+                               chunk, part, out);
+        } else {
             hipLaunchKernelGGL(mfma_kernel<128>, grid, dim3(256), 0, st, *g, *b, layer,
-                               q, n_q, qpk, n_kv, mc, rs, part, counters, out);
+                               q, n_q, qpk, mc, tw, rs, part);
+            hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc,
+                               chunk, part, out);
+        }
         return (int)hipGetLastError();
     }
     const int mc = (ml + kChunkV - 1) / kChunkV;

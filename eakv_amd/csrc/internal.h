@@ -26,7 +26,6 @@ struct eakv_cache {
 
     void  *work;           /* device scratch for staging and partials */
     size_t work_bytes;
-    unsigned *counters;    /* fused-attention chunk counters, kept zero */
 };
 
 /* error side channel (cache.c) */

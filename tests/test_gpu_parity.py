@@ -206,6 +206,31 @@ def test_fused_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
     assert ok, (err, nbad)
 
 
+@pytest.mark.parametrize("d,n_q,L", [(128, 16, 100), (64, 8, 4097), (128, 4, 31)])
+def test_fused_ignores_stale_nonfinite_tail(E, rng, d, n_q, L):
+    """Tokens past seq_len that hold non-finite data (appended without
+    advancing) must not reach the result: a tile that covers them gives them
+    weight exactly 0."""
+    nh, lmax = 4, L + 64
+    g, o = pair(E, 1, nh, d, lmax)
+    data = rng.standard_normal((1, 2, nh, L, d)).astype(np.float32)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    bad = np.full((nh, 40, d), np.nan, np.float32)
+    bad[:, ::3] = np.inf
+    bad[:, 1::3, :5] = -np.inf
+    for kv in (0, 1):
+        g.append(bad, 0, kv, 40)       # at positions L..L+39, seq_len stays L
+        o.append(bad, 0, kv, 40)
+    assert g.seq_len == L
+    q = rng.standard_normal((n_q, d)).astype(np.float32)
+    a = g.attention_fused(q, 0, n_q, nh)
+    b = o.attention_fused(q, 0, n_q, nh)
+    assert np.isfinite(a).all()
+    ok, err, nbad = tol_close(a, b, ATOL, RTOL)
+    assert ok, (err, nbad)
+
+
 def test_fused_batch_device(E, rng):
     from eakv_amd.hipmem import DeviceArray
     nl, nh, d, n_q, lmax = 2, 4, 128, 16, 1100
