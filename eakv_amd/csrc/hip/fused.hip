@@ -42,27 +42,12 @@ namespace {
 // ------------------------------------------------------------------ MFMA
 
 constexpr int kWaves = 4;
-constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
+constexpr int kTT = 32;                 // tokens per tile (one pipeline stage), 2^k >= 32
 #ifndef EAKV_FUSED_BLOCKS_PER_CU
 #define EAKV_FUSED_BLOCKS_PER_CU 3
 #endif
 constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
-
-__device__ __forceinline__ int sext8(int v) { return (int)(int8_t)(v & 0xff); }
-
-// byte p (0 = most significant) of the balanced base-256 digits of z,
-// |z| <= 2^30: z = d3*2^24 + d2*2^16 + d1*2^8 + d0, every digit in [-128,127]
-__device__ __forceinline__ int digit_of(int z, int p)
-{
-    const int d0 = sext8(z);
-    const int z1 = (z - d0) >> 8;
-    const int d1 = sext8(z1);
-    const int z2 = (z1 - d1) >> 8;
-    const int d2 = sext8(z2);
-    const int d3 = (z2 - d2) >> 8;
-    return p == 0 ? d3 : (p == 1 ? d2 : (p == 2 ? d1 : d0));
-}
 
 // Tile geometry.  K: 16-token sub-tiles (one int8 MFMA per 64-dim group).
 // V: a token's packed bytes of one kv head are DW = D/8 dwords; in the V
@@ -77,24 +62,37 @@ struct Geo {
     static constexpr int NK = kTT / 16;        // K sub-tiles per tile
 };
 
-// One lane's share of a pipeline stage: the K bytes, K scale/bias and V
-// scale/bias of one tile (score layout: token 16k + tl), and the packed V
-// dwords of the tile before it (V layout).
+// One lane's share of a pipeline stage in registers: the K bytes of one tile
+// (MFMA B layout) and the packed V dwords of the tile before it (V layout).
+// The stage's K and V scales and biases (of the K tile) go to an LDS slot of
+// the wave (see load_scales).
 template <int D>
 struct Stage {
     static constexpr int GPD = Geo<D>::GPD, NK = Geo<D>::NK, NV = Geo<D>::NV;
     uint2 kw[NK][GPD];
-    float ks[NK][GPD], kb[NK][GPD], vs[NK][GPD], vb[NK][GPD];
     uint32_t vw[NV];
 };
+
+// The scales and biases of one tile for this lane's tokens (score layout:
+// token 16k + tl), read from the LDS slot.
+template <int D>
+struct Scales {
+    float ks[Geo<D>::NK][Geo<D>::GPD], kb[Geo<D>::NK][Geo<D>::GPD];
+    float vs[Geo<D>::NK][Geo<D>::GPD], vb[Geo<D>::NK][Geo<D>::GPD];
+};
+
+// floats of one LDS scale slot: planes ks, kb, vs, vb of a tile
+template <int D>
+constexpr int kSlot = 4 * kTT * (D / 64);
 
 // Buffer resources of the six planes (scalar registers) and this lane's byte
 // offsets at the wave's first token.  A tile is read with buffer loads:
 // resource + lane offset + uniform tile offset + immediate, so a tile costs
 // no per-lane address arithmetic.  Reads past a plane's end return 0.
 struct LaneOffs {
-    __amdgpu_buffer_rsrc_t kw, vw, ks, kb, vs, vb;
-    uint32_t kwo, so, vwo;
+    __amdgpu_buffer_rsrc_t kw, vw, layer;
+    uint32_t kwo, vwo, sco;
+    uint32_t plane[4];      // byte offsets of ks, kb, vs, vb from the K block
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void *p, int64_t bytes)
@@ -125,25 +123,69 @@ __device__ __forceinline__ void load_k(Stage<D> &T, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
     const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
-    const uint32_t ws = du * GPD * 32, ss = du * GPD * 4;
+    const uint32_t ws = du * GPD * 32;
 #pragma unroll
-    for (int k = 0; k < Geo<D>::NK; k++) {
+    for (int k = 0; k < Geo<D>::NK; k++)
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
             T.kw[k][gg] = ldb64(P.kw, P.kwo + (16 * k * GPD + gg) * 32, ws);
-        const uint32_t o = P.so + 16 * k * GPD * 4;
-        if (GPD == 2) {
-            const uint2 a = ldb64(P.ks, o, ss), b = ldb64(P.kb, o, ss);
-            const uint2 c = ldb64(P.vs, o, ss), d = ldb64(P.vb, o, ss);
-            T.ks[k][0] = __uint_as_float(a.x); T.ks[k][GPD - 1] = __uint_as_float(a.y);
-            T.kb[k][0] = __uint_as_float(b.x); T.kb[k][GPD - 1] = __uint_as_float(b.y);
-            T.vs[k][0] = __uint_as_float(c.x); T.vs[k][GPD - 1] = __uint_as_float(c.y);
-            T.vb[k][0] = __uint_as_float(d.x); T.vb[k][GPD - 1] = __uint_as_float(d.y);
-        } else {
-            T.ks[k][0] = __uint_as_float(ldb32(P.ks, o, ss));
-            T.kb[k][0] = __uint_as_float(ldb32(P.kb, o, ss));
-            T.vs[k][0] = __uint_as_float(ldb32(P.vs, o, ss));
-            T.vb[k][0] = __uint_as_float(ldb32(P.vb, o, ss));
+}
+
+// The K and V scales and biases of the tile at dt, straight into the wave's
+// LDS slot (buffer loads to LDS: lane m's dword lands at slot + 4m of the
+// instruction's destination).  Slot layout: plane p in {ks, kb, vs, vb} at
+// p * kTT * GPD floats, then token-major, group-minor, as in the planes.
+// d=128: one instruction per plane (64 dwords = 32 tokens x 2 groups);
+// d=64: two planes per instruction (lanes 32-63 take the second).
+template <int D>
+__device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int dt)
+{
+    constexpr int GPD = D / 64;
+    const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
+    const uint32_t ss = du * GPD * 4;
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+#pragma unroll
+    for (int i = 0; i < 4 / (3 - GPD); i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            P.layer, (lds_ptr)(slot + 64 * i), 4, (int)P.sco,
+            (int)(P.plane[(3 - GPD) * i] + ss), 0, 0);
+}
+
+// Loads per stage: DMA scale loads, then K bytes, then V dwords (fixed by
+// sched barriers).  The compiler does not order LDS reads after buffer loads
+// to LDS, so the reads of a slot are preceded by an explicit wait for every
+// load older than the last kYounger<D> ones: the slot's stage issued its DMA
+// loads first, then kSB<D> register loads, and the next stage (kStage<D>
+// loads) has been issued since.
+template <int D>
+constexpr int kDma = 4 / (3 - D / 64);
+template <int D>
+constexpr int kSB = Geo<D>::NK * (D / 64) + Geo<D>::NV;
+template <int D>
+constexpr int kStage = kDma<D> + kSB<D>;
+
+// s_waitcnt vmcnt(n), no wait on the other counters (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int D>
+__device__ __forceinline__ void read_scales(const float *slot, int tl, Scales<D> &C)
+{
+    constexpr int GPD = D / 64, PS = kTT * GPD;
+#pragma unroll
+    for (int k = 0; k < Geo<D>::NK; k++) {
+        const int e = (16 * k + tl) * GPD;
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) {
+            C.ks[k][gg] = slot[0 * PS + e + gg];
+            C.kb[k][gg] = slot[1 * PS + e + gg];
+            C.vs[k][gg] = slot[2 * PS + e + gg];
+            C.vb[k][gg] = slot[3 * PS + e + gg];
         }
     }
 }
@@ -207,11 +249,12 @@ __device__ __forceinline__ float row_max16(float v)
 }
 
 // Slot of a = p*scale for (group g, head h, token tau of a tile) in a wave's
-// a buffer (GPD x 128 floats).  Written in the score layout, read in the V
-// layout; the swizzle keeps both free of LDS bank conflicts.
+// a buffer (GPD x 4*kTT floats).  Written in the score layout, read in the V
+// layout; the swizzle (bits below 32 only) keeps both free of LDS bank
+// conflicts.
 __device__ __forceinline__ int a_slot(int g, int h, int tau)
 {
-    return g * 128 + ((tau * 4 + h) ^ (g * 16) ^ (((tau >> 3) & 1) * 2));
+    return g * 4 * kTT + ((tau * 4 + h) ^ (g * 16) ^ (((tau >> 3) & 1) * 2));
 }
 
 // K of one tile: per 16-token sub-tile, the digit-row dots of each group on
@@ -237,8 +280,8 @@ __device__ __forceinline__ void k_mfma(const Stage<D> &T, const v4i *A,
 }
 
 template <int D>
-__device__ __forceinline__ float k_recomb(const Stage<D> &T, const v4i *d, int k,
-                                          int dt, int n_tok, float wh, float wl,
+__device__ __forceinline__ float k_recomb(const Scales<D> &T, const v4i *d, int k,
+                                          int dt, int L, float wh, float wl,
                                           const float *bq, int tl)
 {
     float a = 0.0f;
@@ -249,14 +292,14 @@ __device__ __forceinline__ float k_recomb(const Stage<D> &T, const v4i *d, int k
         const float u = fmaf((float)hi, wh, (float)lo * wl);
         a = fmaf(T.ks[k][gg], u, fmaf(T.kb[k][gg], bq[gg], a));
     }
-    return dt + 16 * k + tl < n_tok ? a : -INFINITY;
+    return dt + 16 * k + tl < L ? a : -INFINITY;
 }
 
 // Softmax weights of sub-tile k with the running max m of this lane's head:
 // p = 2^(sc - m) (0 for heads >= G), a = p*scale per group into the a
 // buffer, p*bias per group into bi.  Returns p.
 template <int D>
-__device__ __forceinline__ float p_write(const Stage<D> &T, int k, float sc, float m,
+__device__ __forceinline__ float p_write(const Scales<D> &T, int k, float sc, float m,
                                          bool live, float *abuf, int ho, int tl,
                                          float *bi)
 {
@@ -277,7 +320,7 @@ __device__ __forceinline__ float p_write(const Stage<D> &T, int k, float sc, flo
 // 2^(old - new) and the tile's weights rewritten.
 template <int D>
 __device__ __forceinline__ void softmax_tail(
-    WaveState<D> &S, const Stage<D> &T, const float *sc, bool need, float psum,
+    WaveState<D> &S, const Scales<D> &T, const float *sc, bool need, float psum,
     float *bi, bool live, float *abuf, int ho, int tl)
 {
     constexpr int NK = Geo<D>::NK, GPD = D / 64;
@@ -343,31 +386,37 @@ __device__ __forceinline__ void v_step(WaveState<D> &S, const Stage<D> &T,
         S.acc[e] = __builtin_amdgcn_mfma_f32_4x4x1f32(ar[j], nb[e], S.acc[e], 0, 0, 0);
 }
 
-// tw tokens per wave (a multiple of kTT); a block's chunk is kWaves * tw.
-// Writes the chunk's partial (m, l, o[D]) per q head of its kv head;
-// merge_kernel combines the chunks.
+// Token assignment: nb = gridDim.x blocks share one (sequence, kv head).
+// Its kTT-token tiles are dealt round robin, tile j to block (j / kWaves) % nb
+// and wave j % kWaves, so at any time the waves of a (sequence, kv head) read
+// one contiguous window of every plane (DRAM locality), and a wave's tiles
+// are nb * kWaves tiles apart.  Softmax partials do not depend on which
+// tokens a wave sees.  Each block writes its partial (m, l, o[D]) per q head
+// of its kv head; merge_kernel combines the blocks.
 template <int D>
 __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
-    int n_q, int qpk, int max_chunks, int tw, float rs, float *__restrict__ part)
+    int n_q, int qpk, float rs, float *__restrict__ part)
 {
     constexpr int GPD = D / 64;
     constexpr int DW = Geo<D>::DW, NK = Geo<D>::NK, NV = Geo<D>::NV;
-    __shared__ float a_lds[kWaves][2][GPD * 128];
+    __shared__ float a_lds[kWaves][2][GPD * 4 * kTT];
+    __shared__ float s_lds[kWaves][2][kSlot<D>];
     __shared__ float o_lds[kWaves][4][D];
     __shared__ float m_lds[kWaves][4], l_lds[kWaves][4];
 
-    const int ch = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
-    const int t0 = ch * kWaves * tw;
-    if (t0 >= L) return;            // past this sequence's end: no partial
+    const int n_tiles = (L + kTT - 1) / kTT;
+    if (ch * kWaves >= n_tiles) return;     // no tile for this block: no partial
     // the wave index is wave-uniform: say so, so that every per-wave
     // quantity (token range, tile offsets) stays in scalar registers
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = qpk;                                  // 1..4
-    const int wb = t0 + w * tw;
-    const int n_tok = min(L, wb + tw) - wb;             // may be <= 0
+    const int first = ch * kWaves + w;                  // this wave's first tile
+    const int n_wt = first < n_tiles ? (n_tiles - first + nb * kWaves - 1) / (nb * kWaves) : 0;
+    const int stride = nb * kWaves * kTT;               // tokens between its tiles
     const Planes K = planes_of(g, bt.base[s], layer, 0);
     const Planes V = planes_of(g, bt.base[s], layer, 1);
     const int64_t hbase = (int64_t)kvh * g.gph;
@@ -377,10 +426,72 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // pa = i%4), k-block qq = l/16; k-slot j of group gg holds dim
     // 64gg + 8qq + j (j < 8, low nibbles) or 64gg + 32 + 8qq + (j-8).
     // Rows of heads >= G are zero (their q is read from head 0 and dropped).
+    // The q loads are issued first, then the first two pipeline stages
+    // (further below), so the digit arithmetic waits only for q.
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
     const bool qrow = ha < G;
-    const float *qh = qs + (qrow ? ha : 0) * D;
     float qv[GPD][16];
+    {
+        const float4 *qh4 = (const float4 *)(qs + (qrow ? ha : 0) * D);
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+            for (int h2 = 0; h2 < 2; h2++)
+#pragma unroll
+                for (int v4 = 0; v4 < 2; v4++) {
+                    const float4 f = qh4[(64 * gg + 32 * h2 + 8 * qq) / 4 + v4];
+                    float *d = &qv[gg][8 * h2 + 4 * v4];
+                    d[0] = f.x; d[1] = f.y; d[2] = f.z; d[3] = f.w;
+                }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // score layout: this lane receives the scores of head ho for token tl
+    const int ho = l >> 4, tl = l & 15;
+    const bool live = ho < G;
+    // V layout: lane l = (token slot tv, dword u); u is dword uw of group gv;
+    // x = l%4 is the head row (A) and the column (B) of its 4x4x1 block.
+    const int tv = l / DW, u = l % DW, gv = u / 8, uw = u % 8, x = l & 3;
+
+    LaneOffs P;
+    {
+        const int64_t wbytes = g.max_groups * 32;
+        P.kw = plane_rsrc(K.w, wbytes);
+        P.vw = plane_rsrc(V.w, wbytes);
+        // K and V blocks of the layer are adjacent: one resource for the
+        // scale and bias planes of both
+        P.layer = plane_rsrc(K.w, 2 * g.block_bytes);
+        P.plane[0] = (uint32_t)g.s_off;
+        P.plane[1] = (uint32_t)g.b_off;
+        P.plane[2] = (uint32_t)(g.block_bytes + g.s_off);
+        P.plane[3] = (uint32_t)(g.block_bytes + g.b_off);
+        P.sco = GPD == 2 ? (uint32_t)((hbase + l) * 4)
+                         : (uint32_t)((hbase + (l & 31)) * 4 + (l >> 5) * (g.b_off - g.s_off));
+        const int64_t gk = hbase + (int64_t)tl * GPD;
+        const int64_t gvv = hbase + (int64_t)tv * GPD + gv;
+        P.kwo = (uint32_t)(gk * 32 + qq * 8);
+        P.vwo = (uint32_t)(gvv * 32 + uw * 4);
+    }
+
+    // the first two pipeline stages (see the loop below)
+    const int dt0 = first * kTT;                        // token offset of tile 0
+    const int last = dt0 + (n_wt > 0 ? n_wt - 1 : 0) * stride;   // ... of its last tile
+    Stage<D> sa, sb;
+    float *slot_a = s_lds[w][0], *slot_b = s_lds[w][1];
+    auto load_stage = [&](Stage<D> &T, float *slot, int dt) {
+        load_scales<D>(slot, P, min(dt + stride, last));
+        __builtin_amdgcn_sched_barrier(0);
+        load_k<D>(T, P, min(dt + stride, last));
+        load_v<D>(T, P, min(dt, last));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // unconditional (a wave without tiles reads tile dt0, in bounds or 0), so
+    // the q waits below count the same younger loads on every path
+    load_scales<D>(slot_a, P, dt0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_k<D>(sa, P, dt0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_stage(sb, slot_b, dt0);
+
     float amax = 0.0f;
     float qsum[GPD];
 #pragma unroll
@@ -388,11 +499,9 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         double sum = 0.0;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            const int dim = 64 * gg + (j < 8 ? 8 * qq + j : 32 + 8 * qq + j - 8);
-            const float v = qrow ? qh[dim] : 0.0f;
-            qv[gg][j] = v;
-            amax = fmaxf(amax, fabsf(v));
-            sum += (double)v;
+            qv[gg][j] = qrow ? qv[gg][j] : 0.0f;
+            amax = fmaxf(amax, fabsf(qv[gg][j]));
+            sum += (double)qv[gg][j];
         }
         sum += __shfl_xor(sum, 16, 64);
         sum += __shfl_xor(sum, 32, 64);
@@ -403,20 +512,26 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     int ex;
     frexpf(amax, &ex);            // amax < 2^ex, so |q * 2^(30-ex)| < 2^30
     const int esh = 30 - ex;
+    // Balanced base-256 digits of z = rint(q * 2^esh): with |z| < 2^30,
+    // z + 0x80808080 = sum (d_p + 128) 256^(3-p) with every d_p + 128 in
+    // [0, 255], so digit p is byte 3-p of z + 0x80808080, minus 128 (as an
+    // int8 bit pattern: the byte xor 0x80).
     v4i A[GPD];
+    const uint32_t dsh = 8 * (3 - pa);
 #pragma unroll
-    for (int gg = 0; gg < GPD; gg++) {
-        uint32_t wd[4] = {0, 0, 0, 0};
+    for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int z = (int)rintf(ldexpf(qv[gg][j], esh));
-            wd[j >> 2] |= (uint32_t)(digit_of(z, pa) & 0xff) << (8 * (j & 3));
+        for (int w4 = 0; w4 < 4; w4++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int z = (int)rintf(ldexpf(qv[gg][4 * w4 + b], esh));
+                const uint32_t u = (uint32_t)z + 0x80808080u;
+                word |= ((u >> dsh) & 0xffu) << (8 * b);
+            }
+            A[gg][w4] = (int)(word ^ 0x80808080u);
         }
-        A[gg] = v4i{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
-    }
-    // score layout: this lane receives the scores of head ho for token tl
-    const int ho = l >> 4, tl = l & 15;
-    const bool live = ho < G;
+
     const int esh_o = __shfl(esh, 4 * ho, 64);
     // scores are kept in the log2 domain (times log2(e))
     const float rs2 = rs * EAKV_LOG2E;
@@ -424,23 +539,6 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     float bq[GPD];
 #pragma unroll
     for (int gg = 0; gg < GPD; gg++) bq[gg] = rs2 * __shfl(qsum[gg], 4 * ho, 64);
-
-    // V layout: lane l = (token slot tv, dword u); u is dword uw of group gv;
-    // x = l%4 is the head row (A) and the column (B) of its 4x4x1 block.
-    const int tv = l / DW, u = l % DW, gv = u / 8, uw = u % 8, x = l & 3;
-
-    LaneOffs P;
-    {
-        const int64_t wbytes = g.max_groups * 32, sbytes = g.max_groups * 4;
-        P.kw = plane_rsrc(K.w, wbytes); P.ks = plane_rsrc(K.s, sbytes);
-        P.kb = plane_rsrc(K.b, sbytes); P.vw = plane_rsrc(V.w, wbytes);
-        P.vs = plane_rsrc(V.s, sbytes); P.vb = plane_rsrc(V.b, sbytes);
-        const int64_t gk = hbase + (int64_t)(wb + tl) * GPD;
-        const int64_t gvv = hbase + (int64_t)(wb + tv) * GPD + gv;
-        P.kwo = (uint32_t)(gk * 32 + qq * 8);
-        P.so = (uint32_t)(gk * 4);
-        P.vwo = (uint32_t)(gvv * 32 + uw * 4);
-    }
 
     WaveState<D> S;
 #pragma unroll
@@ -457,15 +555,8 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // current one is consumed.  Loads are unconditional so that every wait
     // counts the same number of younger loads; past the end they re-read
     // the last tile, and K scores past the end are masked.
-    if (n_tok > 0) {
-        const int last = ((n_tok - 1) / kTT) * kTT;
+    if (n_wt > 0) {
         float *ab0 = a_lds[w][0], *ab1 = a_lds[w][1];
-        Stage<D> sa, sb;
-        auto load_stage = [&](Stage<D> &T, int dt) {
-            load_k<D>(T, P, min(dt + kTT, last));
-            load_v<D>(T, P, min(dt, last));
-            __builtin_amdgcn_sched_barrier(0);
-        };
         // One basic block holds V(i), K(i+1) and the common softmax step of
         // tile i+1.  V runs in steps of 8 MFMAs; the K and softmax work is
         // cut into pieces (recombination and weights per sub-tile, the
@@ -473,14 +564,18 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         // work of one fills the matrix-core time of the other.  The sched
         // barriers fix the pieces' order; inside a step the scheduler
         // interleaves freely.
-        auto iter = [&](const Stage<D> &T, int dt, const float *av, float *ak) {
+        auto iter = [&](const Stage<D> &T, const float *slot, int dt, const float *av,
+                        float *ak) {
             constexpr int NP = 2 * NK + 1;
             float ar[NV], sc[NK], bi[GPD], psum = 0.0f;
             bool need = false;
 #pragma unroll
             for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
             v4i dk[NK][GPD];
+            Scales<D> C;
             read_a<D>(av, gv, x, tv, ar);
+            wait_vm<kSB<D> + kStage<D>>();
+            read_scales<D>(slot, tl, C);
             k_mfma<D>(T, A, dk);
 #pragma unroll
             for (int h = 0; h < NV; h++) {
@@ -489,11 +584,11 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
                 for (int piece = 0; piece < NP; piece++) {
                     if (1 + piece * (NV - 1) / NP != h) continue;
                     if (piece < NK) {
-                        sc[piece] = k_recomb<D>(T, dk[piece], piece, dt + kTT, n_tok, wh,
+                        sc[piece] = k_recomb<D>(C, dk[piece], piece, dt + stride, L, wh,
                                                 wl, bq, tl);
                     } else if (piece < 2 * NK) {
                         const int k = piece - NK;
-                        psum += p_write<D>(T, k, sc[k], S.m, live, ak, ho, tl, bi);
+                        psum += p_write<D>(C, k, sc[k], S.m, live, ak, ho, tl, bi);
                     } else {
                         float mt = sc[0];
 #pragma unroll
@@ -503,34 +598,35 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            softmax_tail<D>(S, T, sc, need, psum, bi, live, ak, ho, tl);
+            softmax_tail<D>(S, C, sc, need, psum, bi, live, ak, ho, tl);
         };
-        load_k<D>(sa, P, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_stage(sb, 0);
         {
             float sc[NK], bi[GPD], psum = 0.0f;
             v4i dk[NK][GPD];
 #pragma unroll
             for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
+            Scales<D> C;
+            // slot_a's DMA, then sa's K bytes, then all of sb
+            wait_vm<Geo<D>::NK * GPD + kStage<D>>();
+            read_scales<D>(slot_a, tl, C);
             k_mfma<D>(sa, A, dk);
             float mt = -INFINITY;
 #pragma unroll
             for (int k = 0; k < NK; k++) {
-                sc[k] = k_recomb<D>(sa, dk[k], k, 0, n_tok, wh, wl, bq, tl);
+                sc[k] = k_recomb<D>(C, dk[k], k, dt0, L, wh, wl, bq, tl);
                 mt = fmaxf(mt, sc[k]);
             }
 #pragma unroll
-            for (int k = 0; k < NK; k++) psum += p_write<D>(sa, k, sc[k], S.m, live, ab0, ho, tl, bi);
-            softmax_tail<D>(S, sa, sc, live && mt - S.m > kTau, psum, bi, live, ab0, ho, tl);
+            for (int k = 0; k < NK; k++) psum += p_write<D>(C, k, sc[k], S.m, live, ab0, ho, tl, bi);
+            softmax_tail<D>(S, C, sc, live && mt - S.m > kTau, psum, bi, live, ab0, ho, tl);
         }
-        for (int dt = 0;; dt += 2 * kTT) {
-            load_stage(sa, dt + kTT);
-            iter(sb, dt, ab0, ab1);
-            if (dt + kTT >= n_tok) break;
-            load_stage(sb, dt + 2 * kTT);
-            iter(sa, dt + kTT, ab1, ab0);
-            if (dt + 2 * kTT >= n_tok) break;
+        for (int i = 0, dt = dt0;; i += 2, dt += 2 * stride) {
+            load_stage(sa, slot_a, dt + stride);
+            iter(sb, slot_b, dt, ab0, ab1);
+            if (i + 1 >= n_wt) break;
+            load_stage(sb, slot_b, dt + 2 * stride);
+            iter(sa, slot_a, dt + stride, ab1, ab0);
+            if (i + 2 >= n_wt) break;
         }
     }
 
@@ -585,7 +681,7 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
             lt = fmaf(l_lds[ww][h], f, lt);
             ot = fmaf(o_lds[ww][h][dim], f, ot);
         }
-        float *dst = part + (((int64_t)s * n_q + kvh * qpk + h) * max_chunks + ch) * (D + 2);
+        float *dst = part + (((int64_t)s * n_q + kvh * qpk + h) * nb + ch) * (D + 2);
         dst[2 + dim] = ot;
         if (dim == 0) {
             dst[0] = M;
@@ -595,31 +691,50 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
 }
 
 // Merge of the MFMA program's chunk partials (log2 domain) per (q head,
-// sequence), in chunk order: M = max(-1e6 log2(e), m_c) (the reference's
-// max starts at -1e6), l = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M),
-// out = o * (1/l).  An empty sequence has no chunks: 0 * (1/0) = NaN, as the
-// reference.
+// sequence): M = max(-1e6 log2(e), m_c) (the reference's max starts at
+// -1e6), l = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M), out = o * (1/l).
+// The chunks are read kMergeBatch at a time with all loads in flight and
+// merged online across batches.  An empty sequence has no chunks:
+// 0 * (1/0) = NaN, as the reference.
+constexpr int kMergeBatch = 16;
+
 template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(
-    eakvd_batch bt, int n_q, int max_chunks, int chunk,
-    const float *__restrict__ part, float *__restrict__ out)
+    eakvd_batch bt, int n_q, int max_chunks, const float *__restrict__ part,
+    float *__restrict__ out)
 {
     const int qh = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
-    const int n_chunks = (bt.seq_len[s] + chunk - 1) / chunk;
+    // blocks that had a tile (see mfma_kernel)
+    const int n_tiles = (bt.seq_len[s] + kTT - 1) / kTT;
+    const int n_chunks = min(max_chunks, (n_tiles + kWaves - 1) / kWaves);
     const float *p = part + ((int64_t)s * n_q + qh) * max_chunks * (D + 2);
-    float M = -1000000.0f * EAKV_LOG2E;
-    for (int c = 0; c < n_chunks; c++) M = fmaxf(M, p[c * (D + 2)]);
-    float lt = 0.0f, ot = 0.0f;
-#pragma unroll 4
-    for (int c = 0; c < n_chunks; c++) {
-        const float *pc = p + c * (D + 2);
-        const float f = __builtin_amdgcn_exp2f(pc[0] - M);
-        lt = fmaf(pc[1], f, lt);
-        ot = fmaf(pc[2 + i], f, ot);
+    float M = -1000000.0f * EAKV_LOG2E, lt = 0.0f, ot = 0.0f;
+    for (int c0 = 0; c0 < n_chunks; c0 += kMergeBatch) {
+        float m[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; j++) {
+            const float *pc = p + min(c0 + j, n_chunks - 1) * (D + 2);
+            m[j] = pc[0];
+            lv[j] = pc[1];
+            ov[j] = pc[2 + i];
+        }
+        float Mn = M;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; j++)
+            if (c0 + j < n_chunks) Mn = fmaxf(Mn, m[j]);
+        const float f = __builtin_amdgcn_exp2f(M - Mn);
+        lt *= f;
+        ot *= f;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; j++) {
+            const float wj = c0 + j < n_chunks ? __builtin_amdgcn_exp2f(m[j] - Mn) : 0.0f;
+            lt = fmaf(lv[j], wj, lt);
+            ot = fmaf(ov[j], wj, ot);
+        }
+        M = Mn;
     }
     out[((int64_t)s * n_q + qh) * D + i] = ot * (1.0f / lt);
 }
-
 
 // ------------------------------------------------------------------ VALU
 
@@ -798,12 +913,11 @@ __global__ __launch_bounds__(D) void combine_kernel(
     out[((int64_t)s * n_q + qh) * D + i] = __fmul_rn(o, 1.0f / l);
 }
 
-// Tokens per wave of the MFMA program: enough chunks per (sequence, kv
-// head) that the grid fills every CU with kBlocksPerCU resident blocks once
-// (a second partial round of blocks would idle most of the chip), at least
-// 128 tokens per wave (so chunks are no finer than the workspace allows) and
-// a multiple of the tile.
-int mfma_tokens_per_wave(int ml, int units)
+// Blocks per (sequence, kv head) of the MFMA program: enough that the grid
+// fills every CU with kBlocksPerCU resident blocks once (a second, partial
+// round of blocks would idle most of the chip), no more than the workspace's
+// partials allow (one per kChunkV tokens) and at least one.
+int mfma_blocks_per_unit(int ml, int units)
 {
     static int n_cu = 0;
     if (n_cu == 0) {
@@ -816,10 +930,10 @@ int mfma_tokens_per_wave(int ml, int units)
             n_cu = 256;
     }
     const int slots = n_cu * kBlocksPerCU;
-    const int per_unit = units >= slots ? 1 : slots / units;
-    int tw = (ml + per_unit * kWaves - 1) / (per_unit * kWaves);
-    tw = (tw + kTT - 1) / kTT * kTT;
-    return tw < 128 ? 128 : tw;
+    int nb = units >= slots ? 1 : slots / units;
+    const int cap = (ml + kChunkV - 1) / kChunkV;
+    nb = nb < cap ? nb : cap;
+    return nb < 1 ? 1 : nb;
 }
 
 int max_len(const eakvd_batch *b)
@@ -848,24 +962,23 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
     const float rs = 1.0f / sqrtf((float)g->head_dim);
     float *part = (float *)work;
     const int ml = max_len(b);
-    // the MFMA program addresses a plane with 32-bit buffer offsets
-    const bool small_planes = g->max_groups * 32 <= (int64_t)0x7fffffff;
+    // the MFMA program addresses a layer's K and V blocks with 32-bit buffer
+    // offsets
+    const bool small_planes = 2 * g->block_bytes <= (int64_t)0x7fffffff;
     if (qpk <= 4 && small_planes) {
-        const int tw = mfma_tokens_per_wave(ml, b->n_seq * n_kv);
-        const int chunk = kWaves * tw;
-        const int mc = ml > 0 ? (ml + chunk - 1) / chunk : 1;
+        const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv);
         const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
         const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
         if (g->head_dim == 64) {
             hipLaunchKernelGGL(mfma_kernel<64>, grid, dim3(256), 0, st, *g, *b, layer,
-                               q, n_q, qpk, mc, tw, rs, part);
+                               q, n_q, qpk, rs, part);
             hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc,
-                               chunk, part, out);
+                               part, out);
         } else {
             hipLaunchKernelGGL(mfma_kernel<128>, grid, dim3(256), 0, st, *g, *b, layer,
-                               q, n_q, qpk, mc, tw, rs, part);
+                               q, n_q, qpk, rs, part);
             hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc,
-                               chunk, part, out);
+                               part, out);
         }
         return (int)hipGetLastError();
     }
