@@ -371,19 +371,23 @@ __device__ __forceinline__ void read_a(const float *abuf, int gv, int x, int tv,
     for (int j = 0; j < Geo<D>::NV; j++) ar[j] = abuf[a_slot(gv, x, Geo<D>::TSV * j + tv)];
 }
 
-// One V step of a tile: 8 outer-product MFMAs (one per nibble of this lane's
-// dword), rows a = p*scale of the 4 heads, columns the nibbles as f32.
-template <int D>
-__device__ __forceinline__ void v_step(WaveState<D> &S, const Stage<D> &T,
-                                       const float *ar, int j)
+// One V step of a tile: the 8 nibbles of this lane's dword as f32 (v_cvt),
+// then 8 outer-product MFMAs, rows a = p*scale of the 4 heads, columns the
+// nibbles.  The conversion of step j+1 is issued beside the MFMAs of step j,
+// so no MFMA waits for a conversion just issued.
+__device__ __forceinline__ void v_cvt(uint32_t w, float *nb)
 {
-    const uint32_t lo = nib_lo(T.vw[j]), hi = nib_hi(T.vw[j]);
-    float nb[8];
+    const uint32_t lo = nib_lo(w), hi = nib_hi(w);
 #pragma unroll
     for (int e = 0; e < 8; e++) nb[e] = (float)(((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xffu);
+}
+
+template <int D>
+__device__ __forceinline__ void v_mfma(WaveState<D> &S, const float *nb, float a)
+{
 #pragma unroll
     for (int e = 0; e < 8; e++)
-        S.acc[e] = __builtin_amdgcn_mfma_f32_4x4x1f32(ar[j], nb[e], S.acc[e], 0, 0, 0);
+        S.acc[e] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, nb[e], S.acc[e], 0, 0, 0);
 }
 
 // Token assignment: nb = gridDim.x blocks share one (sequence, kv head).
@@ -577,9 +581,12 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
             wait_vm<kSB<D> + kStage<D>>();
             read_scales<D>(slot, tl, C);
             k_mfma<D>(T, A, dk);
+            float nb[2][8];
+            v_cvt(T.vw[0], nb[0]);
 #pragma unroll
             for (int h = 0; h < NV; h++) {
-                v_step<D>(S, T, ar, h);
+                if (h + 1 < NV) v_cvt(T.vw[h + 1], nb[(h + 1) & 1]);
+                v_mfma<D>(S, nb[h & 1], ar[h]);
 #pragma unroll
                 for (int piece = 0; piece < NP; piece++) {
                     if (1 + piece * (NV - 1) / NP != h) continue;
