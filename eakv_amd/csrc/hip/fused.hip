@@ -6,33 +6,31 @@
 // extended per q head to GQA and d=64.  Each q head h reads kv head
 // h / (n_q/n_kv).
 //
-// Work split (flash-decoding): one block per (sequence, kv head, chunk).
-// Chunk partials (m, l, o[D]) are merged in chunk order by the last block of
-// each (sequence, kv head) to finish (an atomic count, no spinning), so one
-// launch produces the output.
+// Work split (flash-decoding): one block per (sequence, kv head, chunk);
+// each block writes a partial (m, l, o[D]) per q head and merge_kernel
+// combines the chunks.
 //
 // Two block programs:
 //
-// mfma_kernel (up to 4 q heads per kv head): 4 waves x 1024 tokens per block.
-//   Each wave walks its tokens in 32-token tiles, two pipeline stages in
-//   flight (ping-pong registers, buffer loads issued one stage ahead):
-//   K, 16 tokens per v_mfma_i32_16x16x64_i8 and 64-dim group:
-//     A = the q heads as 32-bit fixed point split into four signed bytes
-//         (rows 4h+p: head h, byte p), B = the token's nibbles as int8 (the
-//         packed bytes masked, no conversion).  The exact integer dot of each
-//         byte row is recombined in f32 with weights 2^24, 2^16, 2^8, 1
-//         (times 2^-e/sqrt(d)), and score = s*dot + b*sum(q)/sqrt(d).
-//   Online softmax in the log2 domain with a lazy running max: the running
-//     max of a head moves only when a tile max exceeds it by more than kTau,
-//     so every p = 2^(score - max) stays <= 2^kTau and the accumulators are
-//     rescaled rarely.
-//   The pipeline runs V(i) beside K(i+1): the K loads of a tile are issued
-//     one tile ahead of its V loads.
-//   V, v_mfma_f32_4x4x1f32 outer products: block (group, token slot), rows =
-//     4 heads with A = p*scale, columns = 4 dims with B = nibble as float;
-//     the bias enters as sum p*bias per (head, group).  p moves from the score
-//     layout (lane = head x token) to the V layout through LDS.
-//   Waves are merged in LDS, then chunks across blocks.
+// mfma_kernel (up to 4 q heads per kv head): 4 waves, each walking 32-token
+//   tiles with two pipeline stages in flight.  Both products run on the int8
+//   matrix cores; on gfx950 matrix and vector instructions of a SIMD do not
+//   overlap, so the design minimises their sum:
+//   K: per 16 tokens and 64-dim group one v_mfma_i32_16x16x64_i8, A = the q
+//     heads as 32-bit fixed point split into four signed bytes (rows 4h+p),
+//     B = the token's packed bytes masked to nibbles.  Exact integer dots,
+//     recombined in f32: score = s*(q.n) + b*sum(q).
+//   Online softmax in the log2 domain with a lazy running max (a head's max
+//     moves only when a score exceeds it by more than kTau).
+//   V: per 16 dims one v_mfma_i32_16x16x32_i8 over the tile's 32 tokens,
+//     A = the weights a = p*scale of the 4 heads as 32-bit fixed point with
+//     one exponent per (head, group, tile), split into four signed bytes
+//     (rows 4h+p); B = the V nibbles, tokens along K.  The V bytes reach LDS
+//     by buffer-load-to-LDS and are read back transposed (8 tokens of one
+//     byte column per lane) by ds_read_b64_tr_b8; the digits of a are
+//     exchanged through LDS the same way.  sum p*bias per (head, group) is
+//     kept apart and added at the end.
+//   Waves are merged in LDS, chunks by merge_kernel.
 // valu_kernel (wider groups): one lane per token for K with the reference
 //   arithmetic, then V by dims; same partial/merge scheme.
 #include "common.h"
@@ -42,35 +40,53 @@ namespace {
 // ------------------------------------------------------------------ MFMA
 
 constexpr int kWaves = 4;
-constexpr int kTT = 32;                 // tokens per tile (one pipeline stage), 2^k >= 32
+constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
 #ifndef EAKV_FUSED_BLOCKS_PER_CU
-#define EAKV_FUSED_BLOCKS_PER_CU 3
+#define EAKV_FUSED_BLOCKS_PER_CU 4
 #endif
 constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
 
-// Tile geometry.  K: 16-token sub-tiles (one int8 MFMA per 64-dim group).
-// V: a token's packed bytes of one kv head are DW = D/8 dwords; in the V
-// layout lane l holds dword u = l % DW of token slot T = l / DW, so one V
-// step covers TSV = 64/DW tokens (4 at d=128, 8 at d=64).
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef __attribute__((address_space(3))) v2i *lds_v2i;
+
+// Tile geometry.  A plane stores a token's GPD groups of 32 packed bytes
+// contiguously, so a tile is NCH chunks of 256 bytes (TPC tokens each).
 template <int D>
 struct Geo {
     static constexpr int GPD = D / 64;
-    static constexpr int DW = D / 8;
-    static constexpr int TSV = 64 / DW;
-    static constexpr int NV = kTT / TSV;       // V steps per tile
-    static constexpr int NK = kTT / 16;        // K sub-tiles per tile
+    static constexpr int NK = kTT / 16;            // K sub-tiles of 16 tokens
+    static constexpr int TPC = 8 / GPD;            // tokens per 256-byte chunk
+    static constexpr int NCH = kTT / TPC;          // chunks per tile
+    static constexpr int VSLOT = NCH * 272;        // LDS bytes of one V tile (padded)
+    static constexpr int SSLOT = 4 * kTT * GPD;    // floats of one scale slot
+    static constexpr int ZROWS = GPD * 2 * kTT;    // 8-byte digit rows per tile
 };
 
-// One lane's share of a pipeline stage in registers: the K bytes of one tile
-// (MFMA B layout) and the packed V dwords of the tile before it (V layout).
-// The stage's K and V scales and biases (of the K tile) go to an LDS slot of
-// the wave (see load_scales).
+// LDS byte offset of chunk c of a V tile: a 272-byte pitch, so chunk c
+// starts 16*(c mod 4) bytes past a multiple of 64.  With the transposed reads
+// below, that puts the 64 lanes' 8-byte rows of one read on 32 distinct bank
+// pairs (2 lanes each, the minimum).
+template <int D>
+__device__ __host__ constexpr int vchunk(int c)
+{
+    return 272 * c;
+}
+
+// The tile's token of byte j (0..7) of a V operand in lane group kq
+// (lanes 16kq..16kq+15).  Digits (A) and nibbles (B) use the same order.
+__device__ __forceinline__ int vtok(int kq, int j)
+{
+    return 16 * (j & 1) + 4 * kq + (j >> 1);
+}
+
+// One lane's K bytes of a pipeline stage (MFMA B layout: token 16k + tl of
+// sub-tile k, bytes 8qq..8qq+7 of each group).  The V bytes and the K and V
+// scales and biases of a stage go to LDS.
 template <int D>
 struct Stage {
-    static constexpr int GPD = Geo<D>::GPD, NK = Geo<D>::NK, NV = Geo<D>::NV;
-    uint2 kw[NK][GPD];
-    uint32_t vw[NV];
+    uint2 kw[Geo<D>::NK][Geo<D>::GPD];
 };
 
 // The scales and biases of one tile for this lane's tokens (score layout:
@@ -81,14 +97,10 @@ struct Scales {
     float vs[Geo<D>::NK][Geo<D>::GPD], vb[Geo<D>::NK][Geo<D>::GPD];
 };
 
-// floats of one LDS scale slot: planes ks, kb, vs, vb of a tile
-template <int D>
-constexpr int kSlot = 4 * kTT * (D / 64);
-
-// Buffer resources of the six planes (scalar registers) and this lane's byte
-// offsets at the wave's first token.  A tile is read with buffer loads:
-// resource + lane offset + uniform tile offset + immediate, so a tile costs
-// no per-lane address arithmetic.  Reads past a plane's end return 0.
+// Buffer resources of the planes (scalar registers) and this lane's byte
+// offsets at the wave's first token.  Tile offsets are wave-uniform and go to
+// the scalar soffset operand, so a tile costs no per-lane address arithmetic.
+// Reads past a plane's end return 0.
 struct LaneOffs {
     __amdgpu_buffer_rsrc_t kw, vw, layer;
     uint32_t kwo, vwo, sco;
@@ -108,12 +120,7 @@ __device__ __forceinline__ uint2 ldb64(__amdgpu_buffer_rsrc_t r, uint32_t vo, ui
     return uint2{v[0], v[1]};
 }
 
-__device__ __forceinline__ uint32_t ldb32(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so)
-{
-    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0);
-}
-
-// Loads of the tile at token offset dt of the wave.  A tile can run up to
+// K bytes of the tile at token offset dt of the wave.  A tile can run up to
 // kTT - 1 tokens past the wave's last token; those reads stay inside the
 // plane (or return 0 beyond it), their scores are masked to -inf and their
 // weight is exactly 0.  dt is the same in every lane; readfirstlane makes
@@ -122,28 +129,38 @@ template <int D>
 __device__ __forceinline__ void load_k(Stage<D> &T, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
-    const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
-    const uint32_t ws = du * GPD * 32;
+    const uint32_t ws = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 32;
 #pragma unroll
     for (int k = 0; k < Geo<D>::NK; k++)
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
-            T.kw[k][gg] = ldb64(P.kw, P.kwo + (16 * k * GPD + gg) * 32, ws);
+            T.kw[k][gg] = ldb64(P.kw, P.kwo, ws + (16 * k * GPD + gg) * 32);
 }
 
-// The K and V scales and biases of the tile at dt, straight into the wave's
-// LDS slot (buffer loads to LDS: lane m's dword lands at slot + 4m of the
-// instruction's destination).  Slot layout: plane p in {ks, kb, vs, vb} at
-// p * kTT * GPD floats, then token-major, group-minor, as in the planes.
-// d=128: one instruction per plane (64 dwords = 32 tokens x 2 groups);
-// d=64: two planes per instruction (lanes 32-63 take the second).
+// The V bytes of the tile at dt into a V slot, one 256-byte chunk per
+// instruction (buffer load to LDS: lane m's dword lands at the chunk's LDS
+// start + 4m).
+template <int D>
+__device__ __forceinline__ void load_v(uint8_t *vslot, const LaneOffs &P, int dt)
+{
+    constexpr int GPD = D / 64;
+    const uint32_t ws = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 32;
+#pragma unroll
+    for (int c = 0; c < Geo<D>::NCH; c++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(P.vw, (lds_ptr)(vslot + vchunk<D>(c)), 4,
+                                                 (int)P.vwo, (int)(ws + 256 * c), 0, 0);
+}
+
+// The K and V scales and biases of the tile at dt into a scale slot.  Slot
+// layout: plane p in {ks, kb, vs, vb} at p * kTT * GPD floats, then
+// token-major, group-minor, as in the planes.  d=128: one instruction per
+// plane (64 dwords = 32 tokens x 2 groups); d=64: two planes per instruction
+// (lanes 32-63 take the second).
 template <int D>
 __device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
-    const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
-    const uint32_t ss = du * GPD * 4;
-    typedef __attribute__((address_space(3))) void *lds_ptr;
+    const uint32_t ss = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 4;
 #pragma unroll
     for (int i = 0; i < 4 / (3 - GPD); i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -151,18 +168,16 @@ __device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int 
             (int)(P.plane[(3 - GPD) * i] + ss), 0, 0);
 }
 
-// Loads per stage: DMA scale loads, then K bytes, then V dwords (fixed by
-// sched barriers).  The compiler does not order LDS reads after buffer loads
-// to LDS, so the reads of a slot are preceded by an explicit wait for every
-// load older than the last kYounger<D> ones: the slot's stage issued its DMA
-// loads first, then kSB<D> register loads, and the next stage (kStage<D>
-// loads) has been issued since.
+// Loads per group, in issue order: V chunks, scales, K bytes (fixed by sched
+// barriers).  The compiler does not order LDS reads after buffer loads to
+// LDS, so reads of a slot are preceded by an explicit wait for every load
+// older than the ones that may still be outstanding.
 template <int D>
-constexpr int kDma = 4 / (3 - D / 64);
+constexpr int kDma = 4 / (3 - D / 64);                   // scale loads
 template <int D>
-constexpr int kSB = Geo<D>::NK * (D / 64) + Geo<D>::NV;
+constexpr int kNK = Geo<D>::NK * (D / 64);               // K loads
 template <int D>
-constexpr int kStage = kDma<D> + kSB<D>;
+constexpr int kGroup = Geo<D>::NCH + kDma<D> + kNK<D>;   // loads per group
 
 // s_waitcnt vmcnt(n), no wait on the other counters (gfx9 encoding:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -190,43 +205,10 @@ __device__ __forceinline__ void read_scales(const float *slot, int tl, Scales<D>
     }
 }
 
-template <int D>
-__device__ __forceinline__ void load_v(Stage<D> &T, const LaneOffs &P, int dt)
-{
-    constexpr int GPD = D / 64;
-    const uint32_t du = (uint32_t)__builtin_amdgcn_readfirstlane(dt);
-    const uint32_t ws = du * GPD * 32;
-#pragma unroll
-    for (int j = 0; j < Geo<D>::NV; j++)
-        T.vw[j] = ldb32(P.vw, P.vwo + Geo<D>::TSV * j * GPD * 32, ws);
-}
-
-// State carried across the tiles of one wave.  acc (V layout): lane (T, u)
-// holds, for nibble e of its dword, the partial output of heads r = 0..3.
-// Score layout (lane = head ho x token tl): the running max m of head ho,
-// the softmax denominator lsum and the bias sums sum p*bias per group.
-template <int D>
-struct WaveState {
-    v4f acc[8];
-    float bacc[D / 64];
-    float lsum, m;
-};
-
-// x & 0x0F0F0F0F hidden from the optimizer, so that extracting byte k of the
-// result stays one v_cvt_f32_ubyte<k>
-__device__ __forceinline__ uint32_t nib_lo(uint32_t x)
-{
-    uint32_t r;
-    asm volatile("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(x));
-    return r;
-}
-
-__device__ __forceinline__ uint32_t nib_hi(uint32_t x)
-{
-    uint32_t r;
-    asm volatile("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(x >> 4));
-    return r;
-}
+// The low and high nibbles of four packed bytes, as bytes (int8 MFMA
+// operands: values 0..15)
+__device__ __forceinline__ uint32_t nib_lo(uint32_t x) { return x & 0x0f0f0f0fu; }
+__device__ __forceinline__ uint32_t nib_hi(uint32_t x) { return (x >> 4) & 0x0f0f0f0fu; }
 
 // p * v with 0 * anything = 0 (v_mul_legacy_f32; otherwise IEEE rounding).
 // A tile can cover tokens past the sequence end whose p is 0 but whose stale
@@ -238,23 +220,57 @@ __device__ __forceinline__ float mul_zero(float p, float v)
     return r;
 }
 
+// max / sum over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1); every lane
+// of the row ends with the result.  bound_ctrl lets the compiler fold each
+// move into the DPP form of the operation.
+template <int N>
+__device__ __forceinline__ int dpp_ror(int v)
+{
+    return __builtin_amdgcn_mov_dpp(v, 0x120 + N, 0xf, 0xf, true);
+}
+
 __device__ __forceinline__ float row_max16(float v)
 {
-    // max over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1)
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(dpp_ror<8>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_ror<4>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_ror<2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_ror<1>(__float_as_int(v))));
     return v;
 }
 
-// Slot of a = p*scale for (group g, head h, token tau of a tile) in a wave's
-// a buffer (GPD x 4*kTT floats).  Written in the score layout, read in the V
-// layout; the swizzle (bits below 32 only) keeps both free of LDS bank
-// conflicts.
-__device__ __forceinline__ int a_slot(int g, int h, int tau)
+// the same for values >= +0 (or NaN), whose bit patterns order as integers
+__device__ __forceinline__ float row_max16_pos(float v)
 {
-    return g * 4 * kTT + ((tau * 4 + h) ^ (g * 16) ^ (((tau >> 3) & 1) * 2));
+    int x = __float_as_int(v);
+    x = max(x, dpp_ror<8>(x));
+    x = max(x, dpp_ror<4>(x));
+    x = max(x, dpp_ror<2>(x));
+    x = max(x, dpp_ror<1>(x));
+    return __int_as_float(x);
+}
+
+__device__ __forceinline__ float max_pos(float a, float b)
+{
+    return __int_as_float(max(__float_as_int(a), __float_as_int(b)));
+}
+
+__device__ __forceinline__ float row_sum16(float v)
+{
+    v += __int_as_float(dpp_ror<8>(__float_as_int(v)));
+    v += __int_as_float(dpp_ror<4>(__float_as_int(v)));
+    v += __int_as_float(dpp_ror<2>(__float_as_int(v)));
+    v += __int_as_float(dpp_ror<1>(__float_as_int(v)));
+    return v;
+}
+
+__device__ __forceinline__ v2i tr8(const uint8_t *p)
+{
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i)p);
+}
+
+__device__ __forceinline__ long as_long(v2i v)
+{
+    return __builtin_bit_cast(long, v);
 }
 
 // K of one tile: per 16-token sub-tile, the digit-row dots of each group on
@@ -295,117 +311,50 @@ __device__ __forceinline__ float k_recomb(const Scales<D> &T, const v4i *d, int 
     return dt + 16 * k + tl < L ? a : -INFINITY;
 }
 
-// Softmax weights of sub-tile k with the running max m of this lane's head:
-// p = 2^(sc - m) (0 for heads >= G), a = p*scale per group into the a
-// buffer, p*bias per group into bi.  Returns p.
-template <int D>
-__device__ __forceinline__ float p_write(const Scales<D> &T, int k, float sc, float m,
-                                         bool live, float *abuf, int ho, int tl,
-                                         float *bi)
+// The V accumulation of one (group, 16-byte column block) of a tile: one
+// transposed read gives each lane 8 tokens' bytes at byte column 16*half + n
+// of group g; the low nibbles are dims 64g + 16half + n, the high nibbles
+// dims 64g + 32 + 16half + n.  Each MFMA sums the 32 tokens of the tile; the
+// four digit rows of a head come back in one lane (C[i], weight 256^i) and
+// are recombined as (256*C3 + C2) * 2^(16-E) + (256*C1 + C0) * 2^-E.
+__device__ __forceinline__ float v_recomb(v4i c, float wh, float wl, float acc)
 {
-    const float p = live ? __builtin_amdgcn_exp2f(sc - m) : 0.0f;
-#pragma unroll
-    for (int gg = 0; gg < D / 64; gg++) {
-        abuf[a_slot(gg, ho, 16 * k + tl)] = mul_zero(p, T.vs[k][gg]);
-        bi[gg] += mul_zero(p, T.vb[k][gg]);
-    }
-    return p;
+    const int hi = c[3] * 256 + c[2];
+    const int lo = c[1] * 256 + c[0];
+    return fmaf((float)hi, wh, fmaf((float)lo, wl, acc));
 }
 
-// The tile's softmax bookkeeping once the previous tile's V is accumulated.
-// Lazy rescale: a head's running max moves only when the tile's max exceeds
-// it by more than kTau (so p <= 2^kTau).  The common case (need false in
-// every lane) only adds the tile's sums; otherwise (rare: the first tile,
-// a new larger score) the moved maxima are set, the accumulators scaled by
-// 2^(old - new) and the tile's weights rewritten.
+// State carried across the tiles of one wave.  acc (V output layout): lane
+// (head l/16, column n = l%16) holds dims 64g + 32lh + 16half + n at
+// acc[g][half][lh].  Score layout (lane = head ho x token tl): the running
+// max m of head ho, the softmax denominator lsum and the bias sums
+// sum p*bias per group.  wh/wl: the digit weights of the tile whose digits
+// are in the digit buffer.
 template <int D>
-__device__ __forceinline__ void softmax_tail(
-    WaveState<D> &S, const Scales<D> &T, const float *sc, bool need, float psum,
-    float *bi, bool live, float *abuf, int ho, int tl)
-{
-    constexpr int NK = Geo<D>::NK, GPD = D / 64;
-    if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        float mt = sc[0];
-#pragma unroll
-        for (int k = 1; k < NK; k++) mt = fmaxf(mt, sc[k]);
-        mt = row_max16(mt);
-        const float mn = live && mt > S.m + kTau ? mt : S.m;
-        const float f = live ? __builtin_amdgcn_exp2f(S.m - mn) : 1.0f;
-        S.m = mn;
-        psum = 0.0f;
-#pragma unroll
-        for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < NK; k++) psum += p_write<D>(T, k, sc[k], S.m, live, abuf, ho, tl, bi);
-        S.lsum *= f;
-#pragma unroll
-        for (int gg = 0; gg < GPD; gg++) S.bacc[gg] *= f;
-        const float f0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 0));
-        const float f1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 16));
-        const float f2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 32));
-        const float f3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), 48));
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            S.acc[e][0] *= f0;
-            S.acc[e][1] *= f1;
-            S.acc[e][2] *= f2;
-            S.acc[e][3] *= f3;
-        }
-    }
-    S.lsum += psum;
-#pragma unroll
-    for (int gg = 0; gg < GPD; gg++) S.bacc[gg] += bi[gg];
-}
-
-// This lane's a of every V step of a tile (V layout: group of its dword,
-// head x = l%4, token TSV*j + T).  LDS accesses of one wave complete in
-// order, so the wavefront-scope fences cost no wait; they keep the compiler
-// from moving these reads above the writes of the tile.
-template <int D>
-__device__ __forceinline__ void read_a(const float *abuf, int gv, int x, int tv, float *ar)
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int j = 0; j < Geo<D>::NV; j++) ar[j] = abuf[a_slot(gv, x, Geo<D>::TSV * j + tv)];
-}
-
-// One V step of a tile: the 8 nibbles of this lane's dword as f32 (v_cvt),
-// then 8 outer-product MFMAs, rows a = p*scale of the 4 heads, columns the
-// nibbles.  The conversion of step j+1 is issued beside the MFMAs of step j,
-// so no MFMA waits for a conversion just issued.
-__device__ __forceinline__ void v_cvt(uint32_t w, float *nb)
-{
-    const uint32_t lo = nib_lo(w), hi = nib_hi(w);
-#pragma unroll
-    for (int e = 0; e < 8; e++) nb[e] = (float)(((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xffu);
-}
-
-template <int D>
-__device__ __forceinline__ void v_mfma(WaveState<D> &S, const float *nb, float a)
-{
-#pragma unroll
-    for (int e = 0; e < 8; e++)
-        S.acc[e] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, nb[e], S.acc[e], 0, 0, 0);
-}
+struct WaveState {
+    float acc[D / 64][2][2];
+    float bacc[D / 64];
+    float wh[D / 64], wl[D / 64];
+    float lsum, m;
+};
 
 // Token assignment: nb = gridDim.x blocks share one (sequence, kv head).
 // Its kTT-token tiles are dealt round robin, tile j to block (j / kWaves) % nb
 // and wave j % kWaves, so at any time the waves of a (sequence, kv head) read
-// one contiguous window of every plane (DRAM locality), and a wave's tiles
-// are nb * kWaves tiles apart.  Softmax partials do not depend on which
-// tokens a wave sees.  Each block writes its partial (m, l, o[D]) per q head
-// of its kv head; merge_kernel combines the blocks.
+// one contiguous window of every plane, and a wave's tiles are nb * kWaves
+// tiles apart.  Softmax partials do not depend on which tokens a wave sees.
+// Each block writes its partial (m, l, o[D]) per q head of its kv head;
+// merge_kernel combines the blocks.
 template <int D>
 __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
     int n_q, int qpk, float rs, float *__restrict__ part)
 {
     constexpr int GPD = D / 64;
-    constexpr int DW = Geo<D>::DW, NK = Geo<D>::NK, NV = Geo<D>::NV;
-    __shared__ float a_lds[kWaves][2][GPD * 4 * kTT];
-    __shared__ float s_lds[kWaves][2][kSlot<D>];
+    constexpr int NK = Geo<D>::NK;
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds[kWaves][2][Geo<D>::VSLOT];
+    __shared__ float s_lds[kWaves][2][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t z_lds[kWaves][Geo<D>::ZROWS * 8];
     __shared__ float o_lds[kWaves][4][D];
     __shared__ float m_lds[kWaves][4], l_lds[kWaves][4];
 
@@ -426,12 +375,12 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     const int64_t hbase = (int64_t)kvh * g.gph;
     const float *qs = q + ((int64_t)s * n_q + (int64_t)kvh * qpk) * D;
 
-    // ---- q -> A operands.  Lane l: row i = l%16 (head ha = i/4, digit
+    // ---- q -> A operands of K.  Lane l: row i = l%16 (head ha = i/4, digit
     // pa = i%4), k-block qq = l/16; k-slot j of group gg holds dim
     // 64gg + 8qq + j (j < 8, low nibbles) or 64gg + 32 + 8qq + (j-8).
     // Rows of heads >= G are zero (their q is read from head 0 and dropped).
-    // The q loads are issued first, then the first two pipeline stages
-    // (further below), so the digit arithmetic waits only for q.
+    // The q loads are issued first, then the first two load groups (further
+    // below), so the digit arithmetic waits only for q.
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
     const bool qrow = ha < G;
     float qv[GPD][16];
@@ -452,9 +401,6 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // score layout: this lane receives the scores of head ho for token tl
     const int ho = l >> 4, tl = l & 15;
     const bool live = ho < G;
-    // V layout: lane l = (token slot tv, dword u); u is dword uw of group gv;
-    // x = l%4 is the head row (A) and the column (B) of its 4x4x1 block.
-    const int tv = l / DW, u = l % DW, gv = u / 8, uw = u % 8, x = l & 3;
 
     LaneOffs P;
     {
@@ -470,31 +416,52 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         P.plane[3] = (uint32_t)(g.block_bytes + g.b_off);
         P.sco = GPD == 2 ? (uint32_t)((hbase + l) * 4)
                          : (uint32_t)((hbase + (l & 31)) * 4 + (l >> 5) * (g.b_off - g.s_off));
-        const int64_t gk = hbase + (int64_t)tl * GPD;
-        const int64_t gvv = hbase + (int64_t)tv * GPD + gv;
-        P.kwo = (uint32_t)(gk * 32 + qq * 8);
-        P.vwo = (uint32_t)(gvv * 32 + uw * 4);
+        P.kwo = (uint32_t)((hbase + (int64_t)tl * GPD) * 32 + qq * 8);
+        P.vwo = (uint32_t)(hbase * 32 + 4 * l);
     }
 
-    // the first two pipeline stages (see the loop below)
+    // LDS read/write offsets of this lane (wave-relative, bytes).
+    //   vrd: the row it supplies to a transposed V read: token
+    //        vtok(kq, r'/2) of its lane group kq, bytes 8(r'%2).. of the
+    //        column block (r' = l%16).
+    //   zrd: the digit row it supplies: row (g, hp = r'%2, token vtok(kq, r'/2)).
+    //   zwr: where its digits land: row (g, ho/2, token 16k + tl), dword ho%2.
+    // Digit rows are 8 bytes, [g][hp][token]; row (g, hp, t) holds the digit
+    // words of heads 2hp and 2hp+1.
+    const int kq = l >> 4, rr = l & 15;
+    uint32_t vrd, zrd, zwr;
+    {
+        const int t = vtok(kq, rr >> 1);
+        const int c = t / Geo<D>::TPC;
+        vrd = (uint32_t)(vchunk<D>(c) + 32 * GPD * (t % Geo<D>::TPC) + 8 * (rr & 1));
+        zrd = (uint32_t)(((rr & 1) * kTT + t) * 8);
+        zwr = (uint32_t)(((ho >> 1) * kTT + tl) * 8 + 4 * (ho & 1));
+    }
+    uint8_t *zb = z_lds[w];
+
+    // the first two load groups (see the loop below)
     const int dt0 = first * kTT;                        // token offset of tile 0
     const int last = dt0 + (n_wt > 0 ? n_wt - 1 : 0) * stride;   // ... of its last tile
     Stage<D> sa, sb;
-    float *slot_a = s_lds[w][0], *slot_b = s_lds[w][1];
-    auto load_stage = [&](Stage<D> &T, float *slot, int dt) {
-        load_scales<D>(slot, P, min(dt + stride, last));
+    float *sslot0 = s_lds[w][0], *sslot1 = s_lds[w][1];
+    uint8_t *vslot0 = v_lds[w][0], *vslot1 = v_lds[w][1];
+    // group j: V of tile j-1, then K scales and bytes of tile j
+    auto load_group = [&](Stage<D> &T, float *sslot, uint8_t *vslot, int dtk, int dtv) {
+        load_v<D>(vslot, P, min(dtv, last));
         __builtin_amdgcn_sched_barrier(0);
-        load_k<D>(T, P, min(dt + stride, last));
-        load_v<D>(T, P, min(dt, last));
+        load_scales<D>(sslot, P, min(dtk, last));
+        __builtin_amdgcn_sched_barrier(0);
+        load_k<D>(T, P, min(dtk, last));
         __builtin_amdgcn_sched_barrier(0);
     };
     // unconditional (a wave without tiles reads tile dt0, in bounds or 0), so
-    // the q waits below count the same younger loads on every path
-    load_scales<D>(slot_a, P, dt0);
+    // the waits below count the same younger loads on every path.  Group 0
+    // has no V tile.
+    load_scales<D>(sslot0, P, dt0);
     __builtin_amdgcn_sched_barrier(0);
     load_k<D>(sa, P, dt0);
     __builtin_amdgcn_sched_barrier(0);
-    load_stage(sb, slot_b, dt0);
+    load_group(sb, sslot1, vslot0, dt0 + stride, dt0);
 
     float amax = 0.0f;
     float qsum[GPD];
@@ -539,135 +506,194 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     const int esh_o = __shfl(esh, 4 * ho, 64);
     // scores are kept in the log2 domain (times log2(e))
     const float rs2 = rs * EAKV_LOG2E;
-    const float wl = ldexpf(rs2, -esh_o), wh = ldexpf(rs2, 16 - esh_o);
+    const float kwl = ldexpf(rs2, -esh_o), kwh = ldexpf(rs2, 16 - esh_o);
     float bq[GPD];
 #pragma unroll
     for (int gg = 0; gg < GPD; gg++) bq[gg] = rs2 * __shfl(qsum[gg], 4 * ho, 64);
 
     WaveState<D> S;
 #pragma unroll
-    for (int e = 0; e < 8; e++) S.acc[e] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int gg = 0; gg < GPD; gg++) S.bacc[gg] = 0.0f;
+    for (int gg = 0; gg < GPD; gg++) {
+        S.acc[gg][0][0] = S.acc[gg][0][1] = S.acc[gg][1][0] = S.acc[gg][1][1] = 0.0f;
+        S.bacc[gg] = 0.0f;
+        S.wh[gg] = S.wl[gg] = 0.0f;
+    }
     S.lsum = 0.0f;
     S.m = -INFINITY;
 
-    // Software pipeline over the wave's tiles.  Stage i holds the K (and V
-    // scale/bias) of tile i+1 and the V dwords of tile i; iteration i runs
-    // V(i) beside K(i+1) and its softmax weights.  Two stages are in flight
-    // (ping-pong registers); the next stage's loads are issued before the
-    // current one is consumed.  Loads are unconditional so that every wait
-    // counts the same number of younger loads; past the end they re-read
-    // the last tile, and K scores past the end are masked.
-    if (n_wt > 0) {
-        float *ab0 = a_lds[w][0], *ab1 = a_lds[w][1];
-        // One basic block holds V(i), K(i+1) and the common softmax step of
-        // tile i+1.  V runs in steps of 8 MFMAs; the K and softmax work is
-        // cut into pieces (recombination and weights per sub-tile, the
-        // rescale test) and one piece rides along each V step, so the VALU
-        // work of one fills the matrix-core time of the other.  The sched
-        // barriers fix the pieces' order; inside a step the scheduler
-        // interleaves freely.
-        auto iter = [&](const Stage<D> &T, const float *slot, int dt, const float *av,
-                        float *ak) {
-            constexpr int NP = 2 * NK + 1;
-            float ar[NV], sc[NK], bi[GPD], psum = 0.0f;
-            bool need = false;
+    // The weights of one tile from its scores and the running max m:
+    // p = 2^(sc - m) (0 for heads >= G), psum = sum p, bi = sum p*bias per
+    // group, and a = p*scale per group as fixed point z = trunc(a * 2^E)
+    // with E = 30 - (exponent of the tile's largest a of the head and
+    // group), so 0 <= z < 2^30.  The balanced digits of z go to the digit
+    // rows; wh/wl are 2^(16-E) and 2^-E.
+    auto weights = [&](const Scales<D> &C, const float *sc, float m, float &psum, float *bi) {
+        float p[NK];
+        psum = 0.0f;
 #pragma unroll
-            for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
-            v4i dk[NK][GPD];
-            Scales<D> C;
-            read_a<D>(av, gv, x, tv, ar);
-            wait_vm<kSB<D> + kStage<D>>();
-            read_scales<D>(slot, tl, C);
-            k_mfma<D>(T, A, dk);
-            float nb[2][8];
-            v_cvt(T.vw[0], nb[0]);
+        for (int k = 0; k < NK; k++) {
+            p[k] = live ? __builtin_amdgcn_exp2f(sc[k] - m) : 0.0f;
+            psum += p[k];
+        }
 #pragma unroll
-            for (int h = 0; h < NV; h++) {
-                if (h + 1 < NV) v_cvt(T.vw[h + 1], nb[(h + 1) & 1]);
-                v_mfma<D>(S, nb[h & 1], ar[h]);
-#pragma unroll
-                for (int piece = 0; piece < NP; piece++) {
-                    if (1 + piece * (NV - 1) / NP != h) continue;
-                    if (piece < NK) {
-                        sc[piece] = k_recomb<D>(C, dk[piece], piece, dt + stride, L, wh,
-                                                wl, bq, tl);
-                    } else if (piece < 2 * NK) {
-                        const int k = piece - NK;
-                        psum += p_write<D>(C, k, sc[k], S.m, live, ak, ho, tl, bi);
-                    } else {
-                        float mt = sc[0];
-#pragma unroll
-                        for (int k = 1; k < NK; k++) mt = fmaxf(mt, sc[k]);
-                        need = live && mt - S.m > kTau;
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            softmax_tail<D>(S, C, sc, need, psum, bi, live, ak, ho, tl);
-        };
-        {
-            float sc[NK], bi[GPD], psum = 0.0f;
-            v4i dk[NK][GPD];
-#pragma unroll
-            for (int gg = 0; gg < GPD; gg++) bi[gg] = 0.0f;
-            Scales<D> C;
-            // slot_a's DMA, then sa's K bytes, then all of sb
-            wait_vm<Geo<D>::NK * GPD + kStage<D>>();
-            read_scales<D>(slot_a, tl, C);
-            k_mfma<D>(sa, A, dk);
-            float mt = -INFINITY;
+        for (int gg = 0; gg < GPD; gg++) {
+            float a[NK], am = 0.0f;
+            bi[gg] = 0.0f;
 #pragma unroll
             for (int k = 0; k < NK; k++) {
-                sc[k] = k_recomb<D>(C, dk[k], k, dt0, L, wh, wl, bq, tl);
-                mt = fmaxf(mt, sc[k]);
+                a[k] = mul_zero(p[k], C.vs[k][gg]);
+                bi[gg] += mul_zero(p[k], C.vb[k][gg]);
+                am = max_pos(am, a[k]);
+            }
+            am = row_max16_pos(am);
+            const int E = 30 - __builtin_amdgcn_frexp_expf(am);
+#pragma unroll
+            for (int k = 0; k < NK; k++) {
+                const int z = (int)__builtin_amdgcn_ldexpf(a[k], E);
+                const uint32_t u = ((uint32_t)z + 0x80808080u) ^ 0x80808080u;
+                *(uint32_t *)(zb + zwr + gg * 2 * kTT * 8 + k * 16 * 8) = u;
+            }
+            S.wl[gg] = __builtin_amdgcn_ldexpf(1.0f, -E);
+            S.wh[gg] = __builtin_amdgcn_ldexpf(1.0f, 16 - E);
+        }
+    };
+
+    // The tile's softmax bookkeeping.  Lazy rescale: a head's running max
+    // moves only when a score exceeds it by more than kTau (so p <= 2^kTau).
+    // The common case (need false in every lane) only adds the tile's sums;
+    // otherwise (rare: the first tile, a new larger score) the moved maxima
+    // are set, the accumulators scaled by 2^(old - new) and the tile's
+    // weights recomputed.
+    auto softmax = [&](const Scales<D> &C, const float *sc) {
+        float psum, bi[GPD];
+        float mt = sc[0];
+#pragma unroll
+        for (int k = 1; k < NK; k++) mt = fmaxf(mt, sc[k]);
+        const bool need = live && mt - S.m > kTau;
+        weights(C, sc, S.m, psum, bi);
+        if (__builtin_amdgcn_ballot_w64(need) != 0) {
+            mt = row_max16(mt);
+            const float mn = live && mt > S.m + kTau ? mt : S.m;
+            const float f = live ? __builtin_amdgcn_exp2f(S.m - mn) : 1.0f;
+            S.m = mn;
+            weights(C, sc, S.m, psum, bi);
+            S.lsum *= f;
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) {
+                S.bacc[gg] *= f;
+                S.acc[gg][0][0] *= f;
+                S.acc[gg][0][1] *= f;
+                S.acc[gg][1][0] *= f;
+                S.acc[gg][1][1] *= f;
+            }
+        }
+        S.lsum += psum;
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) S.bacc[gg] += bi[gg];
+    };
+
+    // K(tile at dt) from its stage and scale slot: the scores of the tile.
+    auto kscores = [&](const Stage<D> &T, const Scales<D> &C, int dt, float *sc) {
+        v4i dk[NK][GPD];
+        k_mfma<D>(T, A, dk);
+#pragma unroll
+        for (int k = 0; k < NK; k++) sc[k] = k_recomb<D>(C, dk[k], k, dt, L, kwh, kwl, bq, tl);
+    };
+
+    // V(tile in vslot) with the digits in the digit rows: the transposed
+    // reads first, then the 4*GPD MFMA pairs, then their recombination, so
+    // the MFMA latency is covered by the MFMAs behind it.
+    auto vsum = [&](const uint8_t *vslot) {
+        v2i az[GPD], x[GPD][2];
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) az[gg] = tr8(zb + zrd + gg * 2 * kTT * 8);
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+            for (int half = 0; half < 2; half++)
+                x[gg][half] = tr8(vslot + vrd + 32 * gg + 16 * half);
+        v4i c[GPD][2][2];
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const v2i lo = v2i{(int)nib_lo(x[gg][half][0]), (int)nib_lo(x[gg][half][1])};
+                const v2i hi = v2i{(int)nib_hi(x[gg][half][0]), (int)nib_hi(x[gg][half][1])};
+                c[gg][half][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    as_long(az[gg]), as_long(lo), v4i{0, 0, 0, 0}, 0, 0, 0);
+                c[gg][half][1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    as_long(az[gg]), as_long(hi), v4i{0, 0, 0, 0}, 0, 0, 0);
             }
 #pragma unroll
-            for (int k = 0; k < NK; k++) psum += p_write<D>(C, k, sc[k], S.m, live, ab0, ho, tl, bi);
-            softmax_tail<D>(S, C, sc, live && mt - S.m > kTau, psum, bi, live, ab0, ho, tl);
+        for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+            for (int half = 0; half < 2; half++)
+#pragma unroll
+                for (int lh = 0; lh < 2; lh++)
+                    S.acc[gg][half][lh] =
+                        v_recomb(c[gg][half][lh], S.wh[gg], S.wl[gg], S.acc[gg][half][lh]);
+    };
+
+    // Software pipeline over the wave's tiles.  Load group j holds the V
+    // bytes of tile j-1 and the K bytes and scales of tile j; iteration i
+    // issues group i+2, then runs V(i) (digits written by the previous
+    // iteration) and K(i+1) with its softmax (digits of tile i+1).  Two
+    // groups are in flight (ping-pong registers and LDS slots).  Loads are
+    // unconditional so that every wait counts the same number of younger
+    // loads; past the end they re-read the last tile, and K scores past the
+    // end are masked.
+    if (n_wt > 0) {
+        {
+            float sc[NK];
+            Scales<D> C;
+            // group 0 (scales, K of tile 0) is complete once at most its K
+            // loads and all of group 1 are outstanding
+            wait_vm<kNK<D> + kGroup<D>>();
+            read_scales<D>(sslot0, tl, C);
+            kscores(sa, C, dt0, sc);
+            softmax(C, sc);
         }
+        auto iter = [&](const uint8_t *vslot, const Stage<D> &T, const float *sslot, int dt) {
+            // V(dt): its chunks were the first loads of the previous group
+            wait_vm<kDma<D> + kNK<D> + kGroup<D>>();
+            vsum(vslot);
+            // K(dt + stride): scales, then bytes (the compiler waits for those)
+            float sc[NK];
+            Scales<D> C;
+            wait_vm<kNK<D> + kGroup<D>>();
+            read_scales<D>(sslot, tl, C);
+            kscores(T, C, dt + stride, sc);
+            softmax(C, sc);
+        };
         for (int i = 0, dt = dt0;; i += 2, dt += 2 * stride) {
-            load_stage(sa, slot_a, dt + stride);
-            iter(sb, slot_b, dt, ab0, ab1);
+            load_group(sa, sslot0, vslot1, dt + 2 * stride, dt + stride);
+            iter(vslot0, sb, sslot1, dt);
             if (i + 1 >= n_wt) break;
-            load_stage(sb, slot_b, dt + 2 * stride);
-            iter(sa, slot_a, dt + stride, ab1, ab0);
+            load_group(sb, sslot1, vslot0, dt + 3 * stride, dt + 2 * stride);
+            iter(vslot1, sa, sslot0, dt + stride);
             if (i + 2 >= n_wt) break;
         }
     }
+    // loads into LDS still in flight (the clamped groups past the end) must
+    // land before the block's LDS is reused or released
+    wait_vm<0>();
 
-    // ---- wave epilogue.  acc: sum the token slots (lane bits of tv).
+    // ---- wave epilogue.  lsum and the bias sums over the 16 token lanes of
+    // a head (score layout); lane l then holds head l/16's bias sums, as its
+    // V outputs are head l/16's.
+    S.lsum = row_sum16(S.lsum);
 #pragma unroll
-    for (int o = DW; o < 64; o <<= 1)
+    for (int gg = 0; gg < GPD; gg++) S.bacc[gg] = row_sum16(S.bacc[gg]);
+    {
+        const int n = l & 15, h = l >> 4;
 #pragma unroll
-        for (int e = 0; e < 8; e++)
+        for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) S.acc[e][r] += __shfl_xor(S.acc[e][r], o, 64);
-    // score layout: lsum and the bias sums over the 16 token lanes of a head
+            for (int half = 0; half < 2; half++)
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) {
-        S.lsum += __shfl_xor(S.lsum, o, 64);
-#pragma unroll
-        for (int gg = 0; gg < GPD; gg++) S.bacc[gg] += __shfl_xor(S.bacc[gg], o, 64);
-    }
-    float bsum[4];                                  // head r, this lane's group gv
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        float b = __shfl(S.bacc[0], 16 * r, 64);
-        if (GPD == 2) {
-            const float b1 = __shfl(S.bacc[GPD - 1], 16 * r, 64);
-            b = gv ? b1 : b;
-        }
-        bsum[r] = b;
-    }
-    if (tv == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int dim = 64 * gv + (e < 4 ? 0 : 32) + 4 * uw + (e & 3);
-#pragma unroll
-            for (int r = 0; r < 4; r++) o_lds[w][r][dim] = S.acc[e][r] + bsum[r];
-        }
+                for (int lh = 0; lh < 2; lh++)
+                    o_lds[w][h][64 * gg + 32 * lh + 16 * half + n] =
+                        S.acc[gg][half][lh] + S.bacc[gg];
     }
     if (tl == 0) {
         m_lds[w][ho] = S.m;
