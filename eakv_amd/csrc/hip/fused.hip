@@ -52,26 +52,30 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef __attribute__((address_space(3))) v2i *lds_v2i;
 
 // Tile geometry.  A plane stores a token's GPD groups of 32 packed bytes
-// contiguously, so a tile is NCH chunks of 256 bytes (TPC tokens each).
+// contiguously (a row of RB bytes, UPT 16-byte units).  Loads to LDS move 16
+// bytes per lane, 1 KB per instruction.
 template <int D>
 struct Geo {
     static constexpr int GPD = D / 64;
     static constexpr int NK = kTT / 16;            // K sub-tiles of 16 tokens
-    static constexpr int TPC = 8 / GPD;            // tokens per 256-byte chunk
-    static constexpr int NCH = kTT / TPC;          // chunks per tile
-    static constexpr int VSLOT = NCH * 272;        // LDS bytes of one V tile (padded)
-    static constexpr int SSLOT = 4 * kTT * GPD;    // floats of one scale slot
+    static constexpr int RB = 32 * GPD;            // bytes of a token's row
+    static constexpr int UPT = RB / 16;            // 16-byte units per row
+    static constexpr int TPC = 8 / GPD;            // tokens per 256 bytes
+    static constexpr int NVD = kTT * RB / 1024;    // V loads per tile
+    static constexpr int VSLOT = kTT * RB;         // LDS bytes of one V tile
+    static constexpr int SSLOT = 256;              // floats of one scale slot
     static constexpr int ZROWS = GPD * 2 * kTT;    // 8-byte digit rows per tile
 };
 
-// LDS byte offset of chunk c of a V tile: a 272-byte pitch, so chunk c
-// starts 16*(c mod 4) bytes past a multiple of 64.  With the transposed reads
-// below, that puts the 64 lanes' 8-byte rows of one read on 32 distinct bank
-// pairs (2 lanes each, the minimum).
+// V tile layout in LDS: token rows in order, the 16-byte units of row t
+// permuted by xor with vswz(t) (bits of the token's 4-token / 8-token
+// block).  With the transposed reads below, that puts the 64 lanes' 8-byte
+// rows of one read on 32 distinct bank pairs (2 lanes each, the minimum),
+// and keeps each 16-byte unit whole for the 16-byte loads.
 template <int D>
-__device__ __host__ constexpr int vchunk(int c)
+__device__ __host__ constexpr int vswz(int t)
 {
-    return 272 * c;
+    return (t / Geo<D>::TPC) & (Geo<D>::UPT - 1);
 }
 
 // The tile's token of byte j (0..7) of a V operand in lane group kq
@@ -104,7 +108,6 @@ struct Scales {
 struct LaneOffs {
     __amdgpu_buffer_rsrc_t kw, vw, layer;
     uint32_t kwo, vwo, sco;
-    uint32_t plane[4];      // byte offsets of ks, kb, vs, vb from the K block
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void *p, int64_t bytes)
@@ -137,35 +140,32 @@ __device__ __forceinline__ void load_k(Stage<D> &T, const LaneOffs &P, int dt)
             T.kw[k][gg] = ldb64(P.kw, P.kwo, ws + (16 * k * GPD + gg) * 32);
 }
 
-// The V bytes of the tile at dt into a V slot, one 256-byte chunk per
-// instruction (buffer load to LDS: lane m's dword lands at the chunk's LDS
-// start + 4m).
+// The V bytes of the tile at dt into a V slot, 1 KB per instruction (buffer
+// load to LDS: lane m's 16 bytes land at the instruction's LDS start + 16m;
+// the lane fetches the unit that belongs there, see LaneOffs.vwo).
 template <int D>
 __device__ __forceinline__ void load_v(uint8_t *vslot, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
     const uint32_t ws = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 32;
 #pragma unroll
-    for (int c = 0; c < Geo<D>::NCH; c++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(P.vw, (lds_ptr)(vslot + vchunk<D>(c)), 4,
-                                                 (int)P.vwo, (int)(ws + 256 * c), 0, 0);
+    for (int i = 0; i < Geo<D>::NVD; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(P.vw, (lds_ptr)(vslot + 1024 * i), 16,
+                                                 (int)P.vwo, (int)(ws + 1024 * i), 0, 0);
 }
 
-// The K and V scales and biases of the tile at dt into a scale slot.  Slot
-// layout: plane p in {ks, kb, vs, vb} at p * kTT * GPD floats, then
-// token-major, group-minor, as in the planes.  d=128: one instruction per
-// plane (64 dwords = 32 tokens x 2 groups); d=64: two planes per instruction
-// (lanes 32-63 take the second).
+// The K and V scales and biases of the tile at dt into a scale slot, one
+// instruction.  Slot layout: plane p in {ks, kb, vs, vb} at p * kTT * GPD
+// floats, then token-major, group-minor, as in the planes (lane m fetches
+// 16 bytes of plane m / (8 GPD); at d=64 lanes 32-63 repeat lanes 0-31 into
+// the unused second half of the slot).
 template <int D>
 __device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
     const uint32_t ss = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 4;
-#pragma unroll
-    for (int i = 0; i < 4 / (3 - GPD); i++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            P.layer, (lds_ptr)(slot + 64 * i), 4, (int)P.sco,
-            (int)(P.plane[(3 - GPD) * i] + ss), 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(P.layer, (lds_ptr)slot, 16, (int)P.sco,
+                                             (int)ss, 0, 0);
 }
 
 // Loads per group, in issue order: V chunks, scales, K bytes (fixed by sched
@@ -173,11 +173,11 @@ __device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int 
 // LDS, so reads of a slot are preceded by an explicit wait for every load
 // older than the ones that may still be outstanding.
 template <int D>
-constexpr int kDma = 4 / (3 - D / 64);                   // scale loads
+constexpr int kDma = 1;                                  // scale loads
 template <int D>
 constexpr int kNK = Geo<D>::NK * (D / 64);               // K loads
 template <int D>
-constexpr int kGroup = Geo<D>::NCH + kDma<D> + kNK<D>;   // loads per group
+constexpr int kGroup = Geo<D>::NVD + kDma<D> + kNK<D>;   // loads per group
 
 // s_waitcnt vmcnt(n), no wait on the other counters (gfx9 encoding:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -410,30 +410,37 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         // K and V blocks of the layer are adjacent: one resource for the
         // scale and bias planes of both
         P.layer = plane_rsrc(K.w, 2 * g.block_bytes);
-        P.plane[0] = (uint32_t)g.s_off;
-        P.plane[1] = (uint32_t)g.b_off;
-        P.plane[2] = (uint32_t)(g.block_bytes + g.s_off);
-        P.plane[3] = (uint32_t)(g.block_bytes + g.b_off);
-        P.sco = GPD == 2 ? (uint32_t)((hbase + l) * 4)
-                         : (uint32_t)((hbase + (l & 31)) * 4 + (l >> 5) * (g.b_off - g.s_off));
+        // scale load: lane l fetches bytes 16e.. of plane pl's tile
+        const int pl = GPD == 2 ? l >> 4 : (l & 31) >> 3;
+        const int e = GPD == 2 ? l & 15 : l & 7;
+        const int64_t poff = (pl & 2 ? g.block_bytes : 0) + (pl & 1 ? g.b_off : g.s_off);
+        P.sco = (uint32_t)(poff + hbase * 4 + 16 * e);
         P.kwo = (uint32_t)((hbase + (int64_t)tl * GPD) * 32 + qq * 8);
-        P.vwo = (uint32_t)(hbase * 32 + 4 * l);
+        // V load: lane l's 16 bytes land at unit l of the first 1 KB of the
+        // slot: token t = l / UPT, unit (l % UPT) of the permuted row
+        const int vt = l / Geo<D>::UPT;
+        const int vu = (l % Geo<D>::UPT) ^ vswz<D>(vt);
+        P.vwo = (uint32_t)(hbase * 32 + vt * Geo<D>::RB + 16 * vu);
     }
 
     // LDS read/write offsets of this lane (wave-relative, bytes).
-    //   vrd: the row it supplies to a transposed V read: token
-    //        vtok(kq, r'/2) of its lane group kq, bytes 8(r'%2).. of the
-    //        column block (r' = l%16).
+    //   vrd: the row it supplies to a transposed V read of column block
+    //        (g, half): token vtok(kq, r'/2) of its lane group kq, bytes
+    //        8(r'%2).. of the block's 16-byte unit (r' = l%16).
     //   zrd: the digit row it supplies: row (g, hp = r'%2, token vtok(kq, r'/2)).
     //   zwr: where its digits land: row (g, ho/2, token 16k + tl), dword ho%2.
     // Digit rows are 8 bytes, [g][hp][token]; row (g, hp, t) holds the digit
     // words of heads 2hp and 2hp+1.
     const int kq = l >> 4, rr = l & 15;
-    uint32_t vrd, zrd, zwr;
+    uint32_t vrd[GPD][2], zrd, zwr;
     {
         const int t = vtok(kq, rr >> 1);
-        const int c = t / Geo<D>::TPC;
-        vrd = (uint32_t)(vchunk<D>(c) + 32 * GPD * (t % Geo<D>::TPC) + 8 * (rr & 1));
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+            for (int half = 0; half < 2; half++)
+                vrd[gg][half] = (uint32_t)(t * Geo<D>::RB +
+                                           16 * ((2 * gg + half) ^ vswz<D>(t)) + 8 * (rr & 1));
         zrd = (uint32_t)(((rr & 1) * kTT + t) * 8);
         zwr = (uint32_t)(((ho >> 1) * kTT + tl) * 8 + 4 * (ho & 1));
     }
@@ -611,7 +618,7 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
             for (int half = 0; half < 2; half++)
-                x[gg][half] = tr8(vslot + vrd + 32 * gg + 16 * half);
+                x[gg][half] = tr8(vslot + vrd[gg][half]);
         v4i c[GPD][2][2];
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
