@@ -33,6 +33,8 @@
 //   Waves are merged in LDS, chunks by merge_kernel.
 // valu_kernel (wider groups): one lane per token for K with the reference
 //   arithmetic, then V by dims; same partial/merge scheme.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -46,6 +48,10 @@ constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
 #endif
 constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
+#ifndef EAKV_FUSED_SLOTS
+#define EAKV_FUSED_SLOTS 3
+#endif
+constexpr int kSlots = EAKV_FUSED_SLOTS;  // load groups per wave: one consumed, the rest in flight
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void *lds_ptr;
@@ -338,13 +344,13 @@ struct WaveState {
     float lsum, m;
 };
 
-// Token assignment: nb = gridDim.x blocks share one (sequence, kv head).
-// Its kTT-token tiles are dealt round robin, tile j to block (j / kWaves) % nb
-// and wave j % kWaves, so at any time the waves of a (sequence, kv head) read
-// one contiguous window of every plane, and a wave's tiles are nb * kWaves
-// tiles apart.  Softmax partials do not depend on which tokens a wave sees.
-// Each block writes its partial (m, l, o[D]) per q head of its kv head;
-// merge_kernel combines the blocks.
+// Tile assignment: nb = gridDim.x blocks share one (sequence, kv head), a
+// "unit" of n_tiles kTT-token tiles, dealt round robin: tile j to block
+// (j / kWaves) % nb and wave j % kWaves.  At any time the waves of a unit
+// read one contiguous window of every plane, and a wave's tiles are
+// nb * kWaves tiles apart.  Softmax partials do not depend on which tokens a
+// wave sees.  Each block writes its partial (m, l, o[D]) per q head of its
+// kv head; merge_kernel combines the blocks.
 template <int D>
 __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
@@ -352,11 +358,22 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
 {
     constexpr int GPD = D / 64;
     constexpr int NK = Geo<D>::NK;
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds[kWaves][2][Geo<D>::VSLOT];
-    __shared__ float s_lds[kWaves][2][Geo<D>::SSLOT];
+    // Per wave: kSlots V and scale slots and the digit rows; after the tiles
+    // the wave's V slot 0 holds its outputs o[4][D] and its digit rows its
+    // m[4], l[4] for the block merge.  Every slot is its own variable: the
+    // compiler then knows that a load into one slot does not write another
+    // and does not make reads of a slot wait for younger loads to LDS.
+    static_assert(Geo<D>::VSLOT >= 4 * D * 4, "outputs fit a V slot");
+    static_assert(kSlots <= 4, "slot variables");
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds0[kWaves][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kWaves][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds2[kSlots > 2 ? kWaves : 1][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds3[kSlots > 3 ? kWaves : 1][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds0[kWaves][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds1[kWaves][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? kWaves : 1][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? kWaves : 1][Geo<D>::SSLOT];
     __shared__ __attribute__((aligned(16))) uint8_t z_lds[kWaves][Geo<D>::ZROWS * 8];
-    __shared__ float o_lds[kWaves][4][D];
-    __shared__ float m_lds[kWaves][4], l_lds[kWaves][4];
 
     const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
@@ -368,8 +385,7 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = qpk;                                  // 1..4
     const int first = ch * kWaves + w;                  // this wave's first tile
-    const int n_wt = first < n_tiles ? (n_tiles - first + nb * kWaves - 1) / (nb * kWaves) : 0;
-    const int stride = nb * kWaves * kTT;               // tokens between its tiles
+    const int stride = nb * kWaves;                     // tiles between its tiles
     const Planes K = planes_of(g, bt.base[s], layer, 0);
     const Planes V = planes_of(g, bt.base[s], layer, 1);
     const int64_t hbase = (int64_t)kvh * g.gph;
@@ -445,30 +461,62 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         zwr = (uint32_t)(((ho >> 1) * kTT + tl) * 8 + 4 * (ho & 1));
     }
     uint8_t *zb = z_lds[w];
+    // slot k of this wave (k a constant)
+    auto vslot = [&](auto kc) -> uint8_t * {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k == 0) return v_lds0[w];
+        else if constexpr (k == 1) return v_lds1[w];
+        else if constexpr (k == 2) return v_lds2[w];
+        else return v_lds3[w];
+    };
+    auto sslot = [&](auto kc) -> float * {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k == 0) return s_lds0[w];
+        else if constexpr (k == 1) return s_lds1[w];
+        else if constexpr (k == 2) return s_lds2[w];
+        else return s_lds3[w];
+    };
+    using I0 = std::integral_constant<int, 0>;
 
-    // the first two load groups (see the loop below)
-    const int dt0 = first * kTT;                        // token offset of tile 0
-    const int last = dt0 + (n_wt > 0 ? n_wt - 1 : 0) * stride;   // ... of its last tile
-    Stage<D> sa, sb;
-    float *sslot0 = s_lds[w][0], *sslot1 = s_lds[w][1];
-    uint8_t *vslot0 = v_lds[w][0], *vslot1 = v_lds[w][1];
-    // group j: V of tile j-1, then K scales and bytes of tile j
-    auto load_group = [&](Stage<D> &T, float *sslot, uint8_t *vslot, int dtk, int dtv) {
-        load_v<D>(vslot, P, min(dtv, last));
+    // Tile schedule: tk[j] = T(i + j), the wave's tiles from the current
+    // one on (T(i) = first + i * stride).
+    int tk[kSlots + 1];
+#pragma unroll
+    for (int j = 0; j < kSlots; j++) tk[j] = first + j * stride;
+    // token offset of a tile for loads: past-the-end tiles re-read the
+    // unit's last tile (in bounds; their scores are masked)
+    auto ldt = [&](int t) { return min(t, n_tiles - 1) * kTT; };
+
+    Stage<D> st[kSlots];
+    // group j: V of tile T(j-1) into V slot (j-1) % kSlots, then the scales
+    // and K bytes of tile T(j) into scale slot and stage j % kSlots
+    auto load_group = [&](auto jc, int tv, int tkk) {
+        constexpr int j = decltype(jc)::value;
+        load_v<D>(vslot(std::integral_constant<int, (j + kSlots - 1) % kSlots>{}), P, ldt(tv));
         __builtin_amdgcn_sched_barrier(0);
-        load_scales<D>(sslot, P, min(dtk, last));
+        load_scales<D>(sslot(std::integral_constant<int, j % kSlots>{}), P, ldt(tkk));
         __builtin_amdgcn_sched_barrier(0);
-        load_k<D>(T, P, min(dtk, last));
+        load_k<D>(st[j % kSlots], P, ldt(tkk));
         __builtin_amdgcn_sched_barrier(0);
     };
-    // unconditional (a wave without tiles reads tile dt0, in bounds or 0), so
+    // Unconditional (a wave without tiles reads the unit's last tile), so
     // the waits below count the same younger loads on every path.  Group 0
-    // has no V tile.
-    load_scales<D>(sslot0, P, dt0);
+    // has no V tile; in its place one 256-byte load of tile T(0)'s V bytes
+    // (fetched again by group 1, so no extra memory traffic) goes to the V
+    // slot that iteration 0 fills.  It makes the prologue load every V slot
+    // in the loop's order, which keeps the compiler's wait placement at the
+    // loop head as tight as inside the loop.
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        P.vw, (lds_ptr)vslot(std::integral_constant<int, kSlots - 1>{}), 4, (int)P.vwo,
+        (int)((uint32_t)__builtin_amdgcn_readfirstlane(ldt(tk[0])) * GPD * 32), 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    load_k<D>(sa, P, dt0);
+    load_scales<D>(sslot(I0{}), P, ldt(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
-    load_group(sb, sslot1, vslot0, dt0 + stride, dt0);
+    load_k<D>(st[0], P, ldt(tk[0]));
+    __builtin_amdgcn_sched_barrier(0);
+    load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
+    if constexpr (kSlots > 2) load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
+    if constexpr (kSlots > 3) load_group(std::integral_constant<int, 3>{}, tk[2], tk[3]);
 
     float amax = 0.0f;
     float qsum[GPD];
@@ -608,17 +656,23 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     };
 
     // V(tile in vslot) with the digits in the digit rows: the transposed
-    // reads first, then the 4*GPD MFMA pairs, then their recombination, so
-    // the MFMA latency is covered by the MFMAs behind it.
-    auto vsum = [&](const uint8_t *vslot) {
+    // reads (vread), then the 4*GPD MFMA pairs, then their recombination, so
+    // the MFMA latency is covered by the MFMAs behind it (vsum).
+    struct VRead {
         v2i az[GPD], x[GPD][2];
+    };
+    auto vread = [&](const uint8_t *vslot, VRead &R) {
 #pragma unroll
-        for (int gg = 0; gg < GPD; gg++) az[gg] = tr8(zb + zrd + gg * 2 * kTT * 8);
+        for (int gg = 0; gg < GPD; gg++) R.az[gg] = tr8(zb + zrd + gg * 2 * kTT * 8);
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
             for (int half = 0; half < 2; half++)
-                x[gg][half] = tr8(vslot + vrd[gg][half]);
+                R.x[gg][half] = tr8(vslot + vrd[gg][half]);
+    };
+    auto vsum = [&](const VRead &R) {
+        const auto &az = R.az;
+        const auto &x = R.x;
         v4i c[GPD][2][2];
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
@@ -642,48 +696,61 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     };
 
     // Software pipeline over the wave's tiles.  Load group j holds the V
-    // bytes of tile j-1 and the K bytes and scales of tile j; iteration i
-    // issues group i+2, then runs V(i) (digits written by the previous
-    // iteration) and K(i+1) with its softmax (digits of tile i+1).  Two
-    // groups are in flight (ping-pong registers and LDS slots).  Loads are
-    // unconditional so that every wait counts the same number of younger
-    // loads; past the end they re-read the last tile, and K scores past the
-    // end are masked.
-    if (n_wt > 0) {
+    // bytes of tile T(j-1) and the K bytes and scales of tile T(j).
+    // Iteration i waits for group i+1, reads V(T(i)) and the digits written
+    // by the previous iteration from LDS, issues group i+kSlots, then runs
+    // V(T(i)) and K(T(i+1)) with its softmax (digits of T(i+1)).  kSlots-1
+    // groups stay in flight behind the one consumed (rotating registers and
+    // LDS slots).
+    constexpr int kLater = (kSlots - 1) * kGroup<D>;    // loads of the groups after the oldest
+    constexpr int kEarly = (kSlots - 2) * kGroup<D>;
+    if (tk[0] < n_tiles) {
         {
             float sc[NK];
             Scales<D> C;
-            // group 0 (scales, K of tile 0) is complete once at most its K
-            // loads and all of group 1 are outstanding
-            wait_vm<kNK<D> + kGroup<D>>();
-            read_scales<D>(sslot0, tl, C);
-            kscores(sa, C, dt0, sc);
+            // group 0 (scales, K of T(0)) is complete once at most its K
+            // loads and all later groups are outstanding
+            wait_vm<kNK<D> + kLater>();
+            read_scales<D>(sslot(I0{}), tl, C);
+            kscores(st[0], C, tk[0] * kTT, sc);
             softmax(C, sc);
         }
-        auto iter = [&](const uint8_t *vslot, const Stage<D> &T, const float *sslot, int dt) {
-            // V(dt): its chunks were the first loads of the previous group
-            wait_vm<kDma<D> + kNK<D> + kGroup<D>>();
-            vsum(vslot);
-            // K(dt + stride): scales, then bytes (the compiler waits for those)
+        // iteration i = r (mod kSlots)
+        auto iter = [&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            // V(T(i)): its loads were the first of group i+1
+            wait_vm<kDma<D> + kNK<D> + kEarly>();
+            VRead R;
+            vread(vslot(rc), R);
+            tk[kSlots] = tk[kSlots - 1] + stride;
+            __builtin_amdgcn_sched_barrier(0);
+            load_group(std::integral_constant<int, r + kSlots>{}, tk[kSlots - 1], tk[kSlots]);
+            vsum(R);
+            // K(T(i+1)): scales, then bytes (the compiler waits for those)
             float sc[NK];
             Scales<D> C;
-            wait_vm<kNK<D> + kGroup<D>>();
-            read_scales<D>(sslot, tl, C);
-            kscores(T, C, dt + stride, sc);
+            wait_vm<kNK<D> + kLater>();
+            read_scales<D>(sslot(std::integral_constant<int, (r + 1) % kSlots>{}), tl, C);
+            kscores(st[(r + 1) % kSlots], C, tk[1] * kTT, sc);
             softmax(C, sc);
+            const bool more = tk[1] < n_tiles;
+#pragma unroll
+            for (int j = 0; j < kSlots; j++) tk[j] = tk[j + 1];
+            return more;
         };
-        for (int i = 0, dt = dt0;; i += 2, dt += 2 * stride) {
-            load_group(sa, sslot0, vslot1, dt + 2 * stride, dt + stride);
-            iter(vslot0, sb, sslot1, dt);
-            if (i + 1 >= n_wt) break;
-            load_group(sb, sslot1, vslot0, dt + 3 * stride, dt + 2 * stride);
-            iter(vslot1, sa, sslot0, dt + stride);
-            if (i + 2 >= n_wt) break;
+        for (;;) {
+            if (!iter(std::integral_constant<int, 0>{})) break;
+            if (!iter(std::integral_constant<int, 1>{})) break;
+            if constexpr (kSlots > 2)
+                if (!iter(std::integral_constant<int, 2>{})) break;
+            if constexpr (kSlots > 3)
+                if (!iter(std::integral_constant<int, 3>{})) break;
         }
     }
     // loads into LDS still in flight (the clamped groups past the end) must
     // land before the block's LDS is reused or released
     wait_vm<0>();
+    float(*o_lds)[D] = (float(*)[D])v_lds0[w];        // this wave's o[4][D]
 
     // ---- wave epilogue.  lsum and the bias sums over the 16 token lanes of
     // a head (score layout); lane l then holds head l/16's bias sums, as its
@@ -699,12 +766,13 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
             for (int half = 0; half < 2; half++)
 #pragma unroll
                 for (int lh = 0; lh < 2; lh++)
-                    o_lds[w][h][64 * gg + 32 * lh + 16 * half + n] =
+                    o_lds[h][64 * gg + 32 * lh + 16 * half + n] =
                         S.acc[gg][half][lh] + S.bacc[gg];
     }
     if (tl == 0) {
-        m_lds[w][ho] = S.m;
-        l_lds[w][ho] = S.lsum;
+        float *ml = (float *)z_lds[w];
+        ml[ho] = S.m;
+        ml[4 + ho] = S.lsum;
     }
     __syncthreads();
 
@@ -713,13 +781,14 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         const int h = i / D, dim = i % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ww++) M = fmaxf(M, m_lds[ww][h]);
+        for (int ww = 0; ww < kWaves; ww++) M = fmaxf(M, ((const float *)z_lds[ww])[h]);
         float lt = 0.0f, ot = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < kWaves; ww++) {
-            const float f = __builtin_amdgcn_exp2f(m_lds[ww][h] - M);
-            lt = fmaf(l_lds[ww][h], f, lt);
-            ot = fmaf(o_lds[ww][h][dim], f, ot);
+            const float *ml = (const float *)z_lds[ww];
+            const float f = __builtin_amdgcn_exp2f(ml[h] - M);
+            lt = fmaf(ml[4 + h], f, lt);
+            ot = fmaf(((const float *)v_lds0[ww])[h * D + dim], f, ot);
         }
         float *dst = part + (((int64_t)s * n_q + kvh * qpk + h) * nb + ch) * (D + 2);
         dst[2 + dim] = ot;
