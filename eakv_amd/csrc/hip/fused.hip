@@ -47,6 +47,13 @@ constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
 #define EAKV_FUSED_BLOCKS_PER_CU 4
 #endif
 constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
+#ifndef EAKV_FUSED_BLOCKS_PER_CU_HH2
+#define EAKV_FUSED_BLOCKS_PER_CU_HH2 2
+#endif
+// resident blocks per CU of the kernel for HH quads of q heads per wave (two
+// quads at d = 128 need more registers than four blocks leave a wave)
+template <int D, int HH>
+constexpr int kBlocksPerCUH = HH == 1 || D == 64 ? kBlocksPerCU : EAKV_FUSED_BLOCKS_PER_CU_HH2;
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
 #ifndef EAKV_FUSED_SLOTS
 #define EAKV_FUSED_SLOTS 3
@@ -351,19 +358,26 @@ struct WaveState {
 // nb * kWaves tiles apart.  Softmax partials do not depend on which tokens a
 // wave sees.  Each block writes its partial (m, l, o[D]) per q head of its
 // kv head; merge_kernel combines the blocks.
-template <int D>
-__global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
+//
+// A wave serves the G = qpk <= 4 HH q heads of its kv head as HH quads of
+// four heads: each quad has its own q digits (K MFMA rows), softmax state,
+// digit rows and V MFMAs; the K bytes, the V tile in LDS and the nibbles
+// taken from them are shared, so the planes are read once for all G heads.
+template <int D, int HH>
+__global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
     int n_q, int qpk, float rs, float *__restrict__ part)
 {
     constexpr int GPD = D / 64;
     constexpr int NK = Geo<D>::NK;
-    // Per wave: kSlots V and scale slots and the digit rows; after the tiles
-    // the wave's V slot 0 holds its outputs o[4][D] and its digit rows its
-    // m[4], l[4] for the block merge.  Every slot is its own variable: the
+    // Per wave: kSlots V and scale slots and the digit rows of its HH
+    // quads; after the tiles the wave's V slots 0 (and 1) hold its outputs
+    // o[4][D] of quad 0 (and 1) and its digit rows its m[8], l[8] for the
+    // block merge.  Every slot is its own variable: the
     // compiler then knows that a load into one slot does not write another
     // and does not make reads of a slot wait for younger loads to LDS.
     static_assert(Geo<D>::VSLOT >= 4 * D * 4, "outputs fit a V slot");
+    static_assert(HH == 1 || HH == 2, "one or two quads");
     static_assert(kSlots <= 4, "slot variables");
     __shared__ __attribute__((aligned(16))) uint8_t v_lds0[kWaves][Geo<D>::VSLOT];
     __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kWaves][Geo<D>::VSLOT];
@@ -373,7 +387,7 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     __shared__ __attribute__((aligned(16))) float s_lds1[kWaves][Geo<D>::SSLOT];
     __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? kWaves : 1][Geo<D>::SSLOT];
     __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? kWaves : 1][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t z_lds[kWaves][Geo<D>::ZROWS * 8];
+    __shared__ __attribute__((aligned(16))) uint8_t z_lds[kWaves][HH * Geo<D>::ZROWS * 8];
 
     const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
@@ -383,7 +397,7 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // quantity (token range, tile offsets) stays in scalar registers
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int G = qpk;                                  // 1..4
+    const int G = qpk;                                  // 1..4 HH
     const int first = ch * kWaves + w;                  // this wave's first tile
     const int stride = nb * kWaves;                     // tiles between its tiles
     const Planes K = planes_of(g, bt.base[s], layer, 0);
@@ -394,14 +408,17 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // ---- q -> A operands of K.  Lane l: row i = l%16 (head ha = i/4, digit
     // pa = i%4), k-block qq = l/16; k-slot j of group gg holds dim
     // 64gg + 8qq + j (j < 8, low nibbles) or 64gg + 32 + 8qq + (j-8).
-    // Rows of heads >= G are zero (their q is read from head 0 and dropped).
-    // The q loads are issued first, then the first two load groups (further
-    // below), so the digit arithmetic waits only for q.
+    // Quad hq holds heads 4hq..4hq+3.  Rows of heads >= G are zero (their q
+    // is read from head 0 and dropped).  The q loads are issued first, then
+    // the first two load groups (further below), so the digit arithmetic
+    // waits only for q.
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
-    const bool qrow = ha < G;
-    float qv[GPD][16];
-    {
-        const float4 *qh4 = (const float4 *)(qs + (qrow ? ha : 0) * D);
+    bool qrow[HH];
+    float qv[HH][GPD][16];
+#pragma unroll
+    for (int hq = 0; hq < HH; hq++) {
+        qrow[hq] = 4 * hq + ha < G;
+        const float4 *qh4 = (const float4 *)(qs + (qrow[hq] ? 4 * hq + ha : 0) * D);
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
@@ -409,14 +426,17 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
 #pragma unroll
                 for (int v4 = 0; v4 < 2; v4++) {
                     const float4 f = qh4[(64 * gg + 32 * h2 + 8 * qq) / 4 + v4];
-                    float *d = &qv[gg][8 * h2 + 4 * v4];
+                    float *d = &qv[hq][gg][8 * h2 + 4 * v4];
                     d[0] = f.x; d[1] = f.y; d[2] = f.z; d[3] = f.w;
                 }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // score layout: this lane receives the scores of head ho for token tl
+    // score layout: this lane receives the scores of head 4hq + ho of each
+    // quad for token tl
     const int ho = l >> 4, tl = l & 15;
-    const bool live = ho < G;
+    bool live[HH];
+#pragma unroll
+    for (int hq = 0; hq < HH; hq++) live[hq] = 4 * hq + ho < G;
 
     LaneOffs P;
     {
@@ -518,6 +538,12 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     if constexpr (kSlots > 2) load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
     if constexpr (kSlots > 3) load_group(std::integral_constant<int, 3>{}, tk[2], tk[3]);
 
+    // scores are kept in the log2 domain (times log2(e))
+    const float rs2 = rs * EAKV_LOG2E;
+    v4i A[HH][GPD];
+    float kwl[HH], kwh[HH], bq[HH][GPD];
+#pragma unroll
+    for (int hq = 0; hq < HH; hq++) {
     float amax = 0.0f;
     float qsum[GPD];
 #pragma unroll
@@ -525,9 +551,9 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         double sum = 0.0;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            qv[gg][j] = qrow ? qv[gg][j] : 0.0f;
-            amax = fmaxf(amax, fabsf(qv[gg][j]));
-            sum += (double)qv[gg][j];
+            qv[hq][gg][j] = qrow[hq] ? qv[hq][gg][j] : 0.0f;
+            amax = fmaxf(amax, fabsf(qv[hq][gg][j]));
+            sum += (double)qv[hq][gg][j];
         }
         sum += __shfl_xor(sum, 16, 64);
         sum += __shfl_xor(sum, 32, 64);
@@ -542,7 +568,6 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // z + 0x80808080 = sum (d_p + 128) 256^(3-p) with every d_p + 128 in
     // [0, 255], so digit p is byte 3-p of z + 0x80808080, minus 128 (as an
     // int8 bit pattern: the byte xor 0x80).
-    v4i A[GPD];
     const uint32_t dsh = 8 * (3 - pa);
 #pragma unroll
     for (int gg = 0; gg < GPD; gg++)
@@ -551,30 +576,33 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
             uint32_t word = 0;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
-                const int z = (int)rintf(ldexpf(qv[gg][4 * w4 + b], esh));
+                const int z = (int)rintf(ldexpf(qv[hq][gg][4 * w4 + b], esh));
                 const uint32_t u = (uint32_t)z + 0x80808080u;
                 word |= ((u >> dsh) & 0xffu) << (8 * b);
             }
-            A[gg][w4] = (int)(word ^ 0x80808080u);
+            A[hq][gg][w4] = (int)(word ^ 0x80808080u);
         }
 
     const int esh_o = __shfl(esh, 4 * ho, 64);
-    // scores are kept in the log2 domain (times log2(e))
-    const float rs2 = rs * EAKV_LOG2E;
-    const float kwl = ldexpf(rs2, -esh_o), kwh = ldexpf(rs2, 16 - esh_o);
-    float bq[GPD];
+    kwl[hq] = ldexpf(rs2, -esh_o);
+    kwh[hq] = ldexpf(rs2, 16 - esh_o);
 #pragma unroll
-    for (int gg = 0; gg < GPD; gg++) bq[gg] = rs2 * __shfl(qsum[gg], 4 * ho, 64);
-
-    WaveState<D> S;
-#pragma unroll
-    for (int gg = 0; gg < GPD; gg++) {
-        S.acc[gg][0][0] = S.acc[gg][0][1] = S.acc[gg][1][0] = S.acc[gg][1][1] = 0.0f;
-        S.bacc[gg] = 0.0f;
-        S.wh[gg] = S.wl[gg] = 0.0f;
+    for (int gg = 0; gg < GPD; gg++) bq[hq][gg] = rs2 * __shfl(qsum[gg], 4 * ho, 64);
     }
-    S.lsum = 0.0f;
-    S.m = -INFINITY;
+
+    WaveState<D> S[HH];
+#pragma unroll
+    for (int hq = 0; hq < HH; hq++) {
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) {
+            S[hq].acc[gg][0][0] = S[hq].acc[gg][0][1] = 0.0f;
+            S[hq].acc[gg][1][0] = S[hq].acc[gg][1][1] = 0.0f;
+            S[hq].bacc[gg] = 0.0f;
+            S[hq].wh[gg] = S[hq].wl[gg] = 0.0f;
+        }
+        S[hq].lsum = 0.0f;
+        S[hq].m = -INFINITY;
+    }
 
     // The weights of one tile from its scores and the running max m:
     // p = 2^(sc - m) (0 for heads >= G), psum = sum p, bi = sum p*bias per
@@ -582,12 +610,16 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // with E = 30 - (exponent of the tile's largest a of the head and
     // group), so 0 <= z < 2^30.  The balanced digits of z go to the digit
     // rows; wh/wl are 2^(16-E) and 2^-E.
-    auto weights = [&](const Scales<D> &C, const float *sc, float m, float &psum, float *bi) {
+    auto weights = [&](auto hqc, const Scales<D> &C, const float *sc, float m, float &psum,
+                       float *bi) {
+        constexpr int hq = decltype(hqc)::value;
+        WaveState<D> &Sq = S[hq];
+        uint8_t *zq = zb + hq * Geo<D>::ZROWS * 8;
         float p[NK];
         psum = 0.0f;
 #pragma unroll
         for (int k = 0; k < NK; k++) {
-            p[k] = live ? __builtin_amdgcn_exp2f(sc[k] - m) : 0.0f;
+            p[k] = live[hq] ? __builtin_amdgcn_exp2f(sc[k] - m) : 0.0f;
             psum += p[k];
         }
 #pragma unroll
@@ -606,10 +638,10 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
             for (int k = 0; k < NK; k++) {
                 const int z = (int)__builtin_amdgcn_ldexpf(a[k], E);
                 const uint32_t u = ((uint32_t)z + 0x80808080u) ^ 0x80808080u;
-                *(uint32_t *)(zb + zwr + gg * 2 * kTT * 8 + k * 16 * 8) = u;
+                *(uint32_t *)(zq + zwr + gg * 2 * kTT * 8 + k * 16 * 8) = u;
             }
-            S.wl[gg] = __builtin_amdgcn_ldexpf(1.0f, -E);
-            S.wh[gg] = __builtin_amdgcn_ldexpf(1.0f, 16 - E);
+            Sq.wl[gg] = __builtin_amdgcn_ldexpf(1.0f, -E);
+            Sq.wh[gg] = __builtin_amdgcn_ldexpf(1.0f, 16 - E);
         }
     };
 
@@ -619,51 +651,64 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // otherwise (rare: the first tile, a new larger score) the moved maxima
     // are set, the accumulators scaled by 2^(old - new) and the tile's
     // weights recomputed.
-    auto softmax = [&](const Scales<D> &C, const float *sc) {
+    auto softmax = [&](auto hqc, const Scales<D> &C, const float *sc) {
+        constexpr int hq = decltype(hqc)::value;
+        WaveState<D> &Sq = S[hq];
         float psum, bi[GPD];
         float mt = sc[0];
 #pragma unroll
         for (int k = 1; k < NK; k++) mt = fmaxf(mt, sc[k]);
-        const bool need = live && mt - S.m > kTau;
-        weights(C, sc, S.m, psum, bi);
+        const bool need = live[hq] && mt - Sq.m > kTau;
+        weights(hqc, C, sc, Sq.m, psum, bi);
         if (__builtin_amdgcn_ballot_w64(need) != 0) {
             mt = row_max16(mt);
-            const float mn = live && mt > S.m + kTau ? mt : S.m;
-            const float f = live ? __builtin_amdgcn_exp2f(S.m - mn) : 1.0f;
-            S.m = mn;
-            weights(C, sc, S.m, psum, bi);
-            S.lsum *= f;
+            const float mn = live[hq] && mt > Sq.m + kTau ? mt : Sq.m;
+            const float f = live[hq] ? __builtin_amdgcn_exp2f(Sq.m - mn) : 1.0f;
+            Sq.m = mn;
+            weights(hqc, C, sc, Sq.m, psum, bi);
+            Sq.lsum *= f;
 #pragma unroll
             for (int gg = 0; gg < GPD; gg++) {
-                S.bacc[gg] *= f;
-                S.acc[gg][0][0] *= f;
-                S.acc[gg][0][1] *= f;
-                S.acc[gg][1][0] *= f;
-                S.acc[gg][1][1] *= f;
+                Sq.bacc[gg] *= f;
+                Sq.acc[gg][0][0] *= f;
+                Sq.acc[gg][0][1] *= f;
+                Sq.acc[gg][1][0] *= f;
+                Sq.acc[gg][1][1] *= f;
             }
         }
-        S.lsum += psum;
+        Sq.lsum += psum;
 #pragma unroll
-        for (int gg = 0; gg < GPD; gg++) S.bacc[gg] += bi[gg];
+        for (int gg = 0; gg < GPD; gg++) Sq.bacc[gg] += bi[gg];
     };
 
-    // K(tile at dt) from its stage and scale slot: the scores of the tile.
-    auto kscores = [&](const Stage<D> &T, const Scales<D> &C, int dt, float *sc) {
-        v4i dk[NK][GPD];
-        k_mfma<D>(T, A, dk);
+    // K(tile at dt) from its stage and scale slot: the scores of the tile
+    // for every quad, then each quad's softmax.
+    auto kscores_softmax = [&](const Stage<D> &T, const Scales<D> &C, int dt) {
+        float sc[HH][NK];
 #pragma unroll
-        for (int k = 0; k < NK; k++) sc[k] = k_recomb<D>(C, dk[k], k, dt, L, kwh, kwl, bq, tl);
+        for (int hq = 0; hq < HH; hq++) {
+            v4i dk[NK][GPD];
+            k_mfma<D>(T, A[hq], dk);
+#pragma unroll
+            for (int k = 0; k < NK; k++)
+                sc[hq][k] = k_recomb<D>(C, dk[k], k, dt, L, kwh[hq], kwl[hq], bq[hq], tl);
+        }
+        softmax(std::integral_constant<int, 0>{}, C, sc[0]);
+        if constexpr (HH > 1) softmax(std::integral_constant<int, 1>{}, C, sc[1]);
     };
 
     // V(tile in vslot) with the digits in the digit rows: the transposed
     // reads (vread), then the 4*GPD MFMA pairs, then their recombination, so
     // the MFMA latency is covered by the MFMAs behind it (vsum).
     struct VRead {
-        v2i az[GPD], x[GPD][2];
+        v2i az[HH][GPD], x[GPD][2];
     };
     auto vread = [&](const uint8_t *vslot, VRead &R) {
 #pragma unroll
-        for (int gg = 0; gg < GPD; gg++) R.az[gg] = tr8(zb + zrd + gg * 2 * kTT * 8);
+        for (int hq = 0; hq < HH; hq++)
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++)
+                R.az[hq][gg] = tr8(zb + hq * Geo<D>::ZROWS * 8 + zrd + gg * 2 * kTT * 8);
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
@@ -671,28 +716,38 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
                 R.x[gg][half] = tr8(vslot + vrd[gg][half]);
     };
     auto vsum = [&](const VRead &R) {
-        const auto &az = R.az;
         const auto &x = R.x;
-        v4i c[GPD][2][2];
+        v2i lo[GPD][2], hi[GPD][2];
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
             for (int half = 0; half < 2; half++) {
-                const v2i lo = v2i{(int)nib_lo(x[gg][half][0]), (int)nib_lo(x[gg][half][1])};
-                const v2i hi = v2i{(int)nib_hi(x[gg][half][0]), (int)nib_hi(x[gg][half][1])};
-                c[gg][half][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                    as_long(az[gg]), as_long(lo), v4i{0, 0, 0, 0}, 0, 0, 0);
-                c[gg][half][1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                    as_long(az[gg]), as_long(hi), v4i{0, 0, 0, 0}, 0, 0, 0);
+                lo[gg][half] = v2i{(int)nib_lo(x[gg][half][0]), (int)nib_lo(x[gg][half][1])};
+                hi[gg][half] = v2i{(int)nib_hi(x[gg][half][0]), (int)nib_hi(x[gg][half][1])};
             }
 #pragma unroll
-        for (int gg = 0; gg < GPD; gg++)
+        for (int hq = 0; hq < HH; hq++) {
+            const auto &az = R.az[hq];
+            v4i c[GPD][2][2];
 #pragma unroll
-            for (int half = 0; half < 2; half++)
+            for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
-                for (int lh = 0; lh < 2; lh++)
-                    S.acc[gg][half][lh] =
-                        v_recomb(c[gg][half][lh], S.wh[gg], S.wl[gg], S.acc[gg][half][lh]);
+                for (int half = 0; half < 2; half++) {
+                    c[gg][half][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                        as_long(az[gg]), as_long(lo[gg][half]), v4i{0, 0, 0, 0}, 0, 0, 0);
+                    c[gg][half][1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                        as_long(az[gg]), as_long(hi[gg][half]), v4i{0, 0, 0, 0}, 0, 0, 0);
+                }
+            WaveState<D> &Sq = S[hq];
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+                for (int half = 0; half < 2; half++)
+#pragma unroll
+                    for (int lh = 0; lh < 2; lh++)
+                        Sq.acc[gg][half][lh] = v_recomb(c[gg][half][lh], Sq.wh[gg], Sq.wl[gg],
+                                                        Sq.acc[gg][half][lh]);
+        }
     };
 
     // Software pipeline over the wave's tiles.  Load group j holds the V
@@ -706,14 +761,12 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     constexpr int kEarly = (kSlots - 2) * kGroup<D>;
     if (tk[0] < n_tiles) {
         {
-            float sc[NK];
             Scales<D> C;
             // group 0 (scales, K of T(0)) is complete once at most its K
             // loads and all later groups are outstanding
             wait_vm<kNK<D> + kLater>();
             read_scales<D>(sslot(I0{}), tl, C);
-            kscores(st[0], C, tk[0] * kTT, sc);
-            softmax(C, sc);
+            kscores_softmax(st[0], C, tk[0] * kTT);
         }
         // iteration i = r (mod kSlots)
         auto iter = [&](auto rc) {
@@ -727,12 +780,10 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
             load_group(std::integral_constant<int, r + kSlots>{}, tk[kSlots - 1], tk[kSlots]);
             vsum(R);
             // K(T(i+1)): scales, then bytes (the compiler waits for those)
-            float sc[NK];
             Scales<D> C;
             wait_vm<kNK<D> + kLater>();
             read_scales<D>(sslot(std::integral_constant<int, (r + 1) % kSlots>{}), tl, C);
-            kscores(st[(r + 1) % kSlots], C, tk[1] * kTT, sc);
-            softmax(C, sc);
+            kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * kTT);
             const bool more = tk[1] < n_tiles;
 #pragma unroll
             for (int j = 0; j < kSlots; j++) tk[j] = tk[j + 1];
@@ -750,15 +801,18 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
     // loads into LDS still in flight (the clamped groups past the end) must
     // land before the block's LDS is reused or released
     wait_vm<0>();
-    float(*o_lds)[D] = (float(*)[D])v_lds0[w];        // this wave's o[4][D]
 
     // ---- wave epilogue.  lsum and the bias sums over the 16 token lanes of
-    // a head (score layout); lane l then holds head l/16's bias sums, as its
-    // V outputs are head l/16's.
-    S.lsum = row_sum16(S.lsum);
+    // a head (score layout); lane l then holds head 4hq + l/16's bias sums,
+    // as its V outputs are that head's.  Quad hq's o[4][D] goes to V slot hq
+    // of the wave, m and l of head h to words h and 8 + h of its digit rows.
 #pragma unroll
-    for (int gg = 0; gg < GPD; gg++) S.bacc[gg] = row_sum16(S.bacc[gg]);
-    {
+    for (int hq = 0; hq < HH; hq++) {
+        WaveState<D> &Sq = S[hq];
+        float(*o_lds)[D] = (float(*)[D])(hq == 0 ? v_lds0[w] : v_lds1[w]);
+        Sq.lsum = row_sum16(Sq.lsum);
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) Sq.bacc[gg] = row_sum16(Sq.bacc[gg]);
         const int n = l & 15, h = l >> 4;
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
@@ -767,12 +821,12 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
 #pragma unroll
                 for (int lh = 0; lh < 2; lh++)
                     o_lds[h][64 * gg + 32 * lh + 16 * half + n] =
-                        S.acc[gg][half][lh] + S.bacc[gg];
-    }
-    if (tl == 0) {
-        float *ml = (float *)z_lds[w];
-        ml[ho] = S.m;
-        ml[4 + ho] = S.lsum;
+                        Sq.acc[gg][half][lh] + Sq.bacc[gg];
+        if (tl == 0) {
+            float *ml = (float *)z_lds[w];
+            ml[4 * hq + ho] = Sq.m;
+            ml[8 + 4 * hq + ho] = Sq.lsum;
+        }
     }
     __syncthreads();
 
@@ -787,8 +841,9 @@ __global__ __launch_bounds__(256, kBlocksPerCU) void mfma_kernel(
         for (int ww = 0; ww < kWaves; ww++) {
             const float *ml = (const float *)z_lds[ww];
             const float f = __builtin_amdgcn_exp2f(ml[h] - M);
-            lt = fmaf(ml[4 + h], f, lt);
-            ot = fmaf(((const float *)v_lds0[ww])[h * D + dim], f, ot);
+            lt = fmaf(ml[8 + h], f, lt);
+            const float *o = (const float *)(h < 4 ? v_lds0[ww] : v_lds1[ww]);
+            ot = fmaf(o[(h & 3) * D + dim], f, ot);
         }
         float *dst = part + (((int64_t)s * n_q + kvh * qpk + h) * nb + ch) * (D + 2);
         dst[2 + dim] = ot;
@@ -1026,7 +1081,7 @@ __global__ __launch_bounds__(D) void combine_kernel(
 // fills every CU with kBlocksPerCU resident blocks once (a second, partial
 // round of blocks would idle most of the chip), no more than the workspace's
 // partials allow (one per kChunkV tokens) and at least one.
-int mfma_blocks_per_unit(int ml, int units)
+int mfma_blocks_per_unit(int ml, int units, int per_cu)
 {
     static int n_cu = 0;
     if (n_cu == 0) {
@@ -1038,7 +1093,7 @@ int mfma_blocks_per_unit(int ml, int units)
         else
             n_cu = 256;
     }
-    const int slots = n_cu * kBlocksPerCU;
+    const int slots = n_cu * per_cu;
     int nb = units >= slots ? 1 : slots / units;
     const int cap = (ml + kChunkV - 1) / kChunkV;
     nb = nb < cap ? nb : cap;
@@ -1074,21 +1129,22 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
     // the MFMA program addresses a layer's K and V blocks with 32-bit buffer
     // offsets
     const bool small_planes = 2 * g->block_bytes <= (int64_t)0x7fffffff;
-    if (qpk <= 4 && small_planes) {
-        const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv);
+    if (qpk <= 8 && small_planes) {
+        const int hh = qpk <= 4 ? 1 : 2;
+        const int per_cu = g->head_dim == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
+                                             : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
+        const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv, per_cu);
         const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
         const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
-        if (g->head_dim == 64) {
-            hipLaunchKernelGGL(mfma_kernel<64>, grid, dim3(256), 0, st, *g, *b, layer,
-                               q, n_q, qpk, rs, part);
+        auto kern = g->head_dim == 64 ? (hh == 1 ? mfma_kernel<64, 1> : mfma_kernel<64, 2>)
+                                      : (hh == 1 ? mfma_kernel<128, 1> : mfma_kernel<128, 2>);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, *g, *b, layer, q, n_q, qpk, rs, part);
+        if (g->head_dim == 64)
             hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc,
                                part, out);
-        } else {
-            hipLaunchKernelGGL(mfma_kernel<128>, grid, dim3(256), 0, st, *g, *b, layer,
-                               q, n_q, qpk, rs, part);
+        else
             hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc,
                                part, out);
-        }
         return (int)hipGetLastError();
     }
     const int mc = (ml + kChunkV - 1) / kChunkV;

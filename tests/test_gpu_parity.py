@@ -147,7 +147,7 @@ SHAPES = [  # (n_kv heads in cache, n_q, n_kv used, d, L, lmax)
     (2, 16, 2, 128, 1000, 1024), (4, 4, 4, 64, 1, 4), (4, 8, 2, 128, 257, 260),
     (1, 8, 1, 64, 1025, 1030), (2, 64, 2, 128, 100, 100),
     (8, 32, 8, 128, 4097, 4100), (4, 16, 4, 64, 2049, 2050), (2, 4, 2, 128, 3000, 3000),
-    (2, 6, 2, 64, 700, 704)]
+    (2, 6, 2, 64, 700, 704), (2, 10, 2, 128, 777, 780), (1, 7, 1, 64, 300, 300)]
 
 
 def loaded(E, rng, nh, d, L, lmax, nl=2):
