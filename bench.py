@@ -256,6 +256,39 @@ def copy_calibration(n_bytes, reps=5):
           flush=True)
 
 
+def read_peak(n_bytes, regions=8, reps=3):
+    """Sustained HBM read rate of the synth library's plain streaming read
+    kernel over passes of n_bytes: `regions` separate buffers read back to
+    back (no pass finds its bytes in the last-level cache), best of `reps`
+    rounds; 3 blocks of 256 threads per CU.  Returns GB/s."""
+    from eakv_amd import hipmem as H
+    lib = Synth().lib
+    lib.eakv_synth_read.restype = C.c_int
+    lib.eakv_synth_read.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]
+    n_bytes = (n_bytes + 15) // 16 * 16
+    lib.eakv_synth_cu_count.restype = C.c_int
+    blocks = 3 * (lib.eakv_synth_cu_count() or 256)
+    buf = H.DeviceArray((regions * n_bytes // 4,))
+    buf.zero()
+    H.synchronize()
+    sink = H.DeviceArray((blocks * 256,))
+    e0, e1 = H.Event(), H.Event()
+    best = None
+    for _ in range(reps):
+        e0.record(None)
+        for r in range(regions):
+            rc = lib.eakv_synth_read(buf.ptr + r * n_bytes, n_bytes, sink.ptr, blocks, None)
+            if rc:
+                raise RuntimeError(f"read launch failed: {rc}")
+        e1.record(None)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / regions
+        best = ms if best is None else min(best, ms)
+    buf.free()
+    sink.free()
+    return n_bytes / best / 1e6
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -300,16 +333,15 @@ def main():
     for _ in range(args.warmup):
         w.step()
     H.synchronize()
-    events = [[H.Event(), H.Event()] for _ in range(c["nl"])]
-    fused_ms = []
+    # one event pair per (step, layer): the steps run back to back, the host
+    # waits only after the last one
+    events = [[[H.Event(), H.Event()] for _ in range(c["nl"])] for _ in range(args.steps)]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        w.step(events)
-        events[-1][1].synchronize()
-        fused_ms.append([e0.elapsed_ms(e1) for e0, e1 in events])
+    for k in range(args.steps):
+        w.step(events[k])
     H.synchronize()
     total_s = time.perf_counter() - t0
-    fused = np.array(fused_ms)
+    fused = np.array([[e0.elapsed_ms(e1) for e0, e1 in ev] for ev in events])
     fused_us = float(fused.mean() * 1e3)
     alg = w.fused_bytes()
     achieved = alg / (fused_us * 1e-6) / 1e9
@@ -321,6 +353,9 @@ def main():
     tfile = os.path.join(ROOT, "profiles", f"fused_config{args.config}_traffic.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+
+    read_gbs = read_peak(alg)
+    log(f"bench: plain streaming read of {alg / 1e6:.1f} MB passes: {read_gbs:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -346,7 +381,9 @@ def main():
         "quantize_gbs": round(w.quant_bytes / w.quant_ms / 1e6, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "alg_bytes_per_launch": alg},
+                     "traffic": traffic, "alg_bytes_per_launch": alg,
+                     "measured_read_gbs": round(read_gbs, 1),
+                     "frac_of_measured_read": round(achieved / read_gbs, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

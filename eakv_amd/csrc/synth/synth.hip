@@ -89,7 +89,46 @@ __global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst,
         dst[i] = src[i];
 }
 
+// Plain streaming read, two 16-byte loads in flight per lane, the words
+// xor-folded into one word per thread: the device's sustained read rate for
+// one contiguous region, the practical ceiling of a bandwidth-bound pass.
+__global__ __launch_bounds__(256) void read_kernel(const uint4 *__restrict__ src, int64_t n16,
+                                                   unsigned *__restrict__ sink)
+{
+    const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t nt = (int64_t)gridDim.x * 256;
+    unsigned a = 0;
+    for (int64_t i = tid; i < n16; i += 2 * nt) {
+        const uint4 u = src[i];
+        const uint4 v = i + nt < n16 ? src[i + nt] : uint4{0, 0, 0, 0};
+        a ^= u.x ^ u.y ^ u.z ^ u.w ^ v.x ^ v.y ^ v.z ^ v.w;
+    }
+    sink[tid] = a;
+}
+
 }  // namespace
+
+// Compute units of the current device (0 if the query fails).
+extern "C" int eakv_synth_cu_count(void)
+{
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    return v;
+}
+
+// Reads src[0, n_bytes) once (n_bytes a multiple of 16, src 16-aligned) with
+// `blocks` blocks of 256 threads; sink receives blocks * 256 words.
+extern "C" int eakv_synth_read(const void *src, int64_t n_bytes, unsigned *sink, int blocks,
+                               void *stream)
+{
+    if (n_bytes <= 0 || blocks <= 0) return 0;
+    if ((n_bytes & 15) || ((uintptr_t)src & 15)) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(read_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, (const uint4 *)src, n_bytes / 16, sink);
+    return (int)hipGetLastError();
+}
 
 // dst[0, n_bytes) = src[0, n_bytes); n_bytes a multiple of 16, both 16-aligned.
 extern "C" int eakv_synth_copy(void *dst, const void *src, int64_t n_bytes,
