@@ -47,13 +47,17 @@ constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
 #define EAKV_FUSED_BLOCKS_PER_CU 4
 #endif
 constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
-#ifndef EAKV_FUSED_BLOCKS_PER_CU_HH2
-#define EAKV_FUSED_BLOCKS_PER_CU_HH2 2
-#endif
-// resident blocks per CU of the kernel for HH quads of q heads per wave (two
-// quads at d = 128 need more registers than four blocks leave a wave)
+// Blocks of the kernel for HH quads of q heads per wave.  One quad: blocks
+// of kWaves waves, kBlocksPerCU resident per CU, tiles dealt statically.
+// Two quads: blocks of 8 waves (d = 128: one per CU, 2 waves per SIMD, as
+// the registers allow; d = 64: two) whose waves take their tiles from a
+// block counter in LDS.  A SIMD issues its older wave's instructions first,
+// so with a static deal the wave of the later block ran last, alone on its
+// SIMD; with the counter the waves of a block finish together.
+template <int HH>
+constexpr int kWavesH = HH == 1 ? kWaves : 8;
 template <int D, int HH>
-constexpr int kBlocksPerCUH = HH == 1 || D == 64 ? kBlocksPerCU : EAKV_FUSED_BLOCKS_PER_CU_HH2;
+constexpr int kBlocksPerCUH = HH == 1 ? kBlocksPerCU : (D == 64 ? 2 : 1);
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
 #ifndef EAKV_FUSED_SLOTS
 #define EAKV_FUSED_SLOTS 3
@@ -364,12 +368,13 @@ struct WaveState {
 // digit rows and V MFMAs; the K bytes, the V tile in LDS and the nibbles
 // taken from them are shared, so the planes are read once for all G heads.
 template <int D, int HH>
-__global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
+__global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, HH> / 4)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
     int n_q, int qpk, float rs, float *__restrict__ part)
 {
     constexpr int GPD = D / 64;
     constexpr int NK = Geo<D>::NK;
+    constexpr int NW = kWavesH<HH>;                     // waves per block
     // Per wave: kSlots V and scale slots and the digit rows of its HH
     // quads; after the tiles the wave's V slots 0 (and 1) hold its outputs
     // o[4][D] of quad 0 (and 1) and its digit rows its m[8], l[8] for the
@@ -379,27 +384,32 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
     static_assert(Geo<D>::VSLOT >= 4 * D * 4, "outputs fit a V slot");
     static_assert(HH == 1 || HH == 2, "one or two quads");
     static_assert(kSlots <= 4, "slot variables");
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds0[kWaves][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kWaves][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds2[kSlots > 2 ? kWaves : 1][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds3[kSlots > 3 ? kWaves : 1][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds0[kWaves][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds1[kWaves][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? kWaves : 1][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? kWaves : 1][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t z_lds[kWaves][HH * Geo<D>::ZROWS * 8];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds0[NW][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds1[NW][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds2[kSlots > 2 ? NW : 1][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds3[kSlots > 3 ? NW : 1][Geo<D>::VSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds0[NW][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds1[NW][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? NW : 1][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? NW : 1][Geo<D>::SSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t z_lds[NW][HH * Geo<D>::ZROWS * 8];
+    __shared__ unsigned q_ctr;                          // claimed tiles (two quads)
 
     const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
     const int n_tiles = (L + kTT - 1) / kTT;
-    if (ch * kWaves >= n_tiles) return;     // no tile for this block: no partial
+    if (ch * NW >= n_tiles) return;         // no tile for this block: no partial
+    if constexpr (HH > 1) {
+        if (threadIdx.x == 0) q_ctr = 0;
+        __syncthreads();
+    }
     // the wave index is wave-uniform: say so, so that every per-wave
     // quantity (token range, tile offsets) stays in scalar registers
     const int tid = threadIdx.x, l = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = qpk;                                  // 1..4 HH
-    const int first = ch * kWaves + w;                  // this wave's first tile
-    const int stride = nb * kWaves;                     // tiles between its tiles
+    const int first = ch * NW + w;                      // this wave's first tile
+    const int stride = nb * NW;                         // tiles between its tiles
     const Planes K = planes_of(g, bt.base[s], layer, 0);
     const Planes V = planes_of(g, bt.base[s], layer, 1);
     const int64_t hbase = (int64_t)kvh * g.gph;
@@ -499,10 +509,30 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
     using I0 = std::integral_constant<int, 0>;
 
     // Tile schedule: tk[j] = T(i + j), the wave's tiles from the current
-    // one on (T(i) = first + i * stride).
+    // one on.  T(j) = first + j * stride for j < kSlots; the later tiles
+    // are T(j) = first + j * stride too (one quad), or the block's claims
+    // (two quads): claim c is tile ch*NW + k%NW + (k/NW)*stride with
+    // k = kSlots*NW + c, so a wave's tiles still increase and the block's
+    // tiles are those of its static deal.
     int tk[kSlots + 1];
 #pragma unroll
     for (int j = 0; j < kSlots; j++) tk[j] = first + j * stride;
+    int ring[kSlots];
+    // lane 0 adds 1 to the block counter, the other lanes add 0 to words of
+    // this wave's digit rows (unchanged), so the add needs no branch
+    uint32_t *cptr = l == 0 ? &q_ctr : (uint32_t *)z_lds[w] + l;
+    const uint32_t cinc = l == 0 ? 1u : 0u;
+    auto fetch = [&](int &dst) {
+        if constexpr (HH > 1) {
+            dst = (int)__hip_atomic_fetch_add(cptr, cinc, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_WORKGROUP);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto claimed = [&](int c) {
+        const int k = kSlots * NW + __builtin_amdgcn_readfirstlane(c);
+        return ch * NW + k % NW + (k / NW) * stride;
+    };
     // token offset of a tile for loads: past-the-end tiles re-read the
     // unit's last tile (in bounds; their scores are masked)
     auto ldt = [&](int t) { return min(t, n_tiles - 1) * kTT; };
@@ -534,9 +564,16 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
     __builtin_amdgcn_sched_barrier(0);
     load_k<D>(st[0], P, ldt(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
+    fetch(ring[1]);
     load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
-    if constexpr (kSlots > 2) load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
-    if constexpr (kSlots > 3) load_group(std::integral_constant<int, 3>{}, tk[2], tk[3]);
+    if constexpr (kSlots > 2) {
+        fetch(ring[2]);
+        load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
+    }
+    if constexpr (kSlots > 3) {
+        fetch(ring[3]);
+        load_group(std::integral_constant<int, 3>{}, tk[2], tk[3]);
+    }
 
     // scores are kept in the log2 domain (times log2(e))
     const float rs2 = rs * EAKV_LOG2E;
@@ -645,40 +682,54 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
         }
     };
 
-    // The tile's softmax bookkeeping.  Lazy rescale: a head's running max
-    // moves only when a score exceeds it by more than kTau (so p <= 2^kTau).
-    // The common case (need false in every lane) only adds the tile's sums;
-    // otherwise (rare: the first tile, a new larger score) the moved maxima
-    // are set, the accumulators scaled by 2^(old - new) and the tile's
-    // weights recomputed.
-    auto softmax = [&](auto hqc, const Scales<D> &C, const float *sc) {
-        constexpr int hq = decltype(hqc)::value;
-        WaveState<D> &Sq = S[hq];
-        float psum, bi[GPD];
-        float mt = sc[0];
+    // The tile's softmax bookkeeping for every quad.  Lazy rescale: a
+    // head's running max moves only when a score exceeds it by more than
+    // kTau (so p <= 2^kTau).  One ballot over all quads: in the common case
+    // (no lane needs a move) the code runs straight through both quads'
+    // weights; otherwise (rare: the first tile, a new larger score) the
+    // moved maxima are set and the accumulators scaled by 2^(old - new)
+    // first.
+    auto softmax = [&](const Scales<D> &C, float (*sc)[NK]) {
+        bool need[HH];
+        float mt[HH];
+        bool any = false;
 #pragma unroll
-        for (int k = 1; k < NK; k++) mt = fmaxf(mt, sc[k]);
-        const bool need = live[hq] && mt - Sq.m > kTau;
-        weights(hqc, C, sc, Sq.m, psum, bi);
-        if (__builtin_amdgcn_ballot_w64(need) != 0) {
-            mt = row_max16(mt);
-            const float mn = live[hq] && mt > Sq.m + kTau ? mt : Sq.m;
-            const float f = live[hq] ? __builtin_amdgcn_exp2f(Sq.m - mn) : 1.0f;
-            Sq.m = mn;
-            weights(hqc, C, sc, Sq.m, psum, bi);
-            Sq.lsum *= f;
+        for (int hq = 0; hq < HH; hq++) {
+            mt[hq] = sc[hq][0];
 #pragma unroll
-            for (int gg = 0; gg < GPD; gg++) {
-                Sq.bacc[gg] *= f;
-                Sq.acc[gg][0][0] *= f;
-                Sq.acc[gg][0][1] *= f;
-                Sq.acc[gg][1][0] *= f;
-                Sq.acc[gg][1][1] *= f;
+            for (int k = 1; k < NK; k++) mt[hq] = fmaxf(mt[hq], sc[hq][k]);
+            need[hq] = live[hq] && mt[hq] - S[hq].m > kTau;
+            any = any || need[hq];
+        }
+        if (__builtin_amdgcn_ballot_w64(any) != 0) {
+#pragma unroll
+            for (int hq = 0; hq < HH; hq++) {
+                WaveState<D> &Sq = S[hq];
+                const float rm = row_max16(mt[hq]);
+                const float mn = live[hq] && rm > Sq.m + kTau ? rm : Sq.m;
+                const float f = live[hq] ? __builtin_amdgcn_exp2f(Sq.m - mn) : 1.0f;
+                Sq.m = mn;
+                Sq.lsum *= f;
+#pragma unroll
+                for (int gg = 0; gg < GPD; gg++) {
+                    Sq.bacc[gg] *= f;
+                    Sq.acc[gg][0][0] *= f;
+                    Sq.acc[gg][0][1] *= f;
+                    Sq.acc[gg][1][0] *= f;
+                    Sq.acc[gg][1][1] *= f;
+                }
             }
         }
-        Sq.lsum += psum;
+        float psum[HH], bi[HH][GPD];
+        weights(std::integral_constant<int, 0>{}, C, sc[0], S[0].m, psum[0], bi[0]);
+        if constexpr (HH > 1)
+            weights(std::integral_constant<int, 1>{}, C, sc[1], S[1].m, psum[1], bi[1]);
 #pragma unroll
-        for (int gg = 0; gg < GPD; gg++) Sq.bacc[gg] += bi[gg];
+        for (int hq = 0; hq < HH; hq++) {
+            S[hq].lsum += psum[hq];
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) S[hq].bacc[gg] += bi[hq][gg];
+        }
     };
 
     // K(tile at dt) from its stage and scale slot: the scores of the tile
@@ -693,8 +744,7 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
             for (int k = 0; k < NK; k++)
                 sc[hq][k] = k_recomb<D>(C, dk[k], k, dt, L, kwh[hq], kwl[hq], bq[hq], tl);
         }
-        softmax(std::integral_constant<int, 0>{}, C, sc[0]);
-        if constexpr (HH > 1) softmax(std::integral_constant<int, 1>{}, C, sc[1]);
+        softmax(C, sc);
     };
 
     // V(tile in vslot) with the digits in the digit rows: the transposed
@@ -775,7 +825,13 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
             wait_vm<kDma<D> + kNK<D> + kEarly>();
             VRead R;
             vread(vslot(rc), R);
-            tk[kSlots] = tk[kSlots - 1] + stride;
+            if constexpr (HH == 1) {
+                tk[kSlots] = tk[kSlots - 1] + stride;
+            } else {
+                tk[kSlots] = claimed(ring[(r + 1) % kSlots]);
+                __builtin_amdgcn_sched_barrier(0);
+                fetch(ring[r]);
+            }
             __builtin_amdgcn_sched_barrier(0);
             load_group(std::integral_constant<int, r + kSlots>{}, tk[kSlots - 1], tk[kSlots]);
             vsum(R);
@@ -786,7 +842,7 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
             kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * kTT);
             const bool more = tk[1] < n_tiles;
 #pragma unroll
-            for (int j = 0; j < kSlots; j++) tk[j] = tk[j + 1];
+            for (int j = 0; j < kSlots; j++) tk[j] = __builtin_amdgcn_readfirstlane(tk[j + 1]);
             return more;
         };
         for (;;) {
@@ -831,14 +887,14 @@ __global__ __launch_bounds__(256, (kBlocksPerCUH<D, HH>)) void mfma_kernel(
     __syncthreads();
 
     // ---- merge the waves into this chunk's partial
-    for (int i = tid; i < G * D; i += 256) {
+    for (int i = tid; i < G * D; i += 64 * NW) {
         const int h = i / D, dim = i % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ww++) M = fmaxf(M, ((const float *)z_lds[ww])[h]);
+        for (int ww = 0; ww < NW; ww++) M = fmaxf(M, ((const float *)z_lds[ww])[h]);
         float lt = 0.0f, ot = 0.0f;
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ww++) {
+        for (int ww = 0; ww < NW; ww++) {
             const float *ml = (const float *)z_lds[ww];
             const float f = __builtin_amdgcn_exp2f(ml[h] - M);
             lt = fmaf(ml[8 + h], f, lt);
@@ -864,13 +920,13 @@ constexpr int kMergeBatch = 16;
 
 template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(
-    eakvd_batch bt, int n_q, int max_chunks, const float *__restrict__ part,
+    eakvd_batch bt, int n_q, int max_chunks, int wpb, const float *__restrict__ part,
     float *__restrict__ out)
 {
     const int qh = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
-    // blocks that had a tile (see mfma_kernel)
+    // blocks that had a tile (see mfma_kernel; wpb waves per block)
     const int n_tiles = (bt.seq_len[s] + kTT - 1) / kTT;
-    const int n_chunks = min(max_chunks, (n_tiles + kWaves - 1) / kWaves);
+    const int n_chunks = min(max_chunks, (n_tiles + wpb - 1) / wpb);
     const float *p = part + ((int64_t)s * n_q + qh) * max_chunks * (D + 2);
     float M = -1000000.0f * EAKV_LOG2E, lt = 0.0f, ot = 0.0f;
     for (int c0 = 0; c0 < n_chunks; c0 += kMergeBatch) {
@@ -1133,17 +1189,19 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         const int hh = qpk <= 4 ? 1 : 2;
         const int per_cu = g->head_dim == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
                                              : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
+        const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
         const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv, per_cu);
         const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
         const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
         auto kern = g->head_dim == 64 ? (hh == 1 ? mfma_kernel<64, 1> : mfma_kernel<64, 2>)
                                       : (hh == 1 ? mfma_kernel<128, 1> : mfma_kernel<128, 2>);
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, *g, *b, layer, q, n_q, qpk, rs, part);
+        hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, qpk, rs,
+                           part);
         if (g->head_dim == 64)
-            hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc,
+            hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc, wpb,
                                part, out);
         else
-            hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc,
+            hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc, wpb,
                                part, out);
         return (int)hipGetLastError();
     }
