@@ -291,6 +291,45 @@ def read_peak(n_bytes, regions=8, reps=3):
     return n_bytes / best / 1e6
 
 
+def dequant_bench(w, steps, warmup):
+    """Whole-plane dequantization (eakv_dequantize_range_device) of every
+    (layer, kv) block of the first cache, back to back into one f32 buffer:
+    40 B read (nibbles, scale, bias) and 256 B written per group.  Returns
+    the JSON line."""
+    E, H, c = w.E, w.H, w.cfg
+    cache = w.caches[0]
+    ng = c["nkv"] * w.lmax * c["d"] // 64
+    out = H.DeviceArray((ng, 64))
+    L = E.lib()
+    planes = [(l, kv) for l in range(c["nl"]) for kv in range(2)]
+
+    def one_pass():
+        for l, kv in planes:
+            rc = L.eakv_dequantize_range_device(cache.h, l, kv, 0, ng, out.ptr, None)
+            assert rc == 0, E.last_error()
+
+    for _ in range(warmup):
+        one_pass()
+    H.synchronize()
+    e0, e1 = H.Event(), H.Event()
+    e0.record(w.stream)
+    for _ in range(steps):
+        one_pass()
+    e1.record(w.stream)
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / (steps * len(planes))
+    alg = ng * (40 + 256)
+    gbs = alg / (us * 1e-6) / 1e9
+    return {"metric": "plane dequantize to f32 GB/s (40 B read + 256 B written per group)",
+            "value": round(gbs, 1), "unit": "GB/s", "higher_is_better": True,
+            "us_per_plane": round(us, 3), "groups_per_plane": ng, "planes_per_step": len(planes),
+            "steps": steps, "n_gpus": 1, "dtype": "q4_1 -> f32",
+            "config": {"workload": c["name"], "plane": f"{c['nkv']} kv heads x {w.lmax} tokens x d{c['d']}"},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "alg_bytes_per_launch": alg}}
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -309,6 +348,9 @@ def main():
     ap.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
     ap.add_argument("--ctx", type=int, default=None, help="override context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--dequant", action="store_true",
+                    help="only time whole-plane dequantization of the first cache, "
+                         "print its JSON line, then exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB, 5 times (the "
                          "known-size kernel for HBM byte counters), then exit")
@@ -329,6 +371,9 @@ def main():
     w.fill_context()
     w.prepare_step_inputs()
     H.synchronize()
+    if args.dequant:
+        print(json.dumps(dequant_bench(w, max(1, args.steps // 4), 1)), flush=True)
+        return
     log(f"bench: quantize {w.quant_bytes / 1e9:.2f} GB alg in {w.quant_ms:.2f} ms "
         f"({w.quant_bytes / w.quant_ms / 1e6:.0f} GB/s)")
 

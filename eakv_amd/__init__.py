@@ -70,6 +70,10 @@ SIGNATURES = {
     "eakv_attention_fused": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "eakv_attention_fused_batch_device": (
         C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "eakv_dequantize_range_device": (
+        C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp, _vp]),
+    "eakv_dequantize_range": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp]),
+    "eakv_validate": (C.c_int, [_vp, _vp]),
 }
 
 _LIB = None
@@ -239,6 +243,19 @@ class Cache:
         b = np.zeros(ng, np.float32)
         _check(lib().eakv_cache_read_planes(self.h, layer, kv_idx, _ptr(w), _ptr(s), _ptr(b)))
         return w, s, b
+
+    def dequantize_range(self, layer, kv_idx, group_start, group_count):
+        """f32[group_count][64] of plane groups [group_start, +group_count)."""
+        out = np.zeros((group_count, 64), np.float32)
+        _check(lib().eakv_dequantize_range(self.h, layer, kv_idx, group_start, group_count,
+                                           _ptr(out)))
+        return out
+
+    def validate(self):
+        """int32[n_layers * 2]: the integrity code of every (layer, kv) block."""
+        res = np.zeros(2 * self.n_layers, np.int32)
+        _check(lib().eakv_validate(self.h, _ptr(res)))
+        return res
 
     def sync(self):
         return _check(lib().eakv_cache_sync(self.h))

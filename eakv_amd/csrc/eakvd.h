@@ -109,6 +109,16 @@ int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
                 const float *q, int n_q, int n_kv, float *out, void *work,
                 void *stream);
 
+/* ---- whole-plane kernels (hip/planes.hip)
+ * eakvd_dequantize: groups [g0, g0 + n) of block (layer, kv) to out
+ * (f32[n][64], device).  eakvd_validate: the integrity check of the first n
+ * groups of each of the n_blocks blocks; res (device, n_blocks words) gets
+ * per block the minimum of g*4 + code over its failing groups, or all ones. */
+int eakvd_dequantize(const eakvd_geom *g, const uint8_t *base, int layer, int kv,
+                     int64_t g0, int64_t n, float *out, void *stream);
+int eakvd_validate(const eakvd_geom *g, const uint8_t *base, int n_blocks,
+                   int64_t n, unsigned long long *res, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

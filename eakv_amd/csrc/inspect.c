@@ -1,0 +1,89 @@
+/* inspect.c — whole-plane reads of a GPU-resident cache: dequantization to
+ * f32 (reference kernels/dequantize_avx512.ea, used by the reference's
+ * benchmark baseline, benchmarks/bench_libeakv.c:76-98) and the integrity
+ * check (reference kernels/validate.ea, run per block by the `validate`
+ * command, src/cli.c:39-98). */
+#include <stdlib.h>
+#include <string.h>
+
+#include "internal.h"
+
+static int deq_args_ok(const eakv_cache_t *c, int layer, int kv_idx,
+                       int64_t group_start, int64_t group_count)
+{
+    return c && layer >= 0 && layer < c->n_layers && kv_idx >= 0 && kv_idx <= 1 &&
+           group_start >= 0 && group_count >= 0 &&
+           group_start <= c->geom.max_groups - group_count;
+}
+
+int eakv_dequantize_range_device(const eakv_cache_t *c, int layer, int kv_idx,
+                                 int64_t group_start, int64_t group_count,
+                                 float *d_out, void *stream)
+{
+    if (!deq_args_ok(c, layer, kv_idx, group_start, group_count) ||
+        (group_count > 0 && !d_out))
+        return eakvi_set_error(EAKV_ERR_INVALID, "dequantize_range: invalid argument");
+    int prev, rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    int e = eakvd_dequantize(&c->geom, c->dev, layer, kv_idx, group_start, group_count,
+                             d_out, eakvi_stream_or_default(c, stream));
+    if (e) rc = eakvi_hip_fail(e, "dequantize_range");
+    eakvi_leave(prev);
+    return rc;
+}
+
+int eakv_dequantize_range(const eakv_cache_t *cc, int layer, int kv_idx,
+                          int64_t group_start, int64_t group_count, float *out)
+{
+    eakv_cache_t *c = (eakv_cache_t *)cc;
+    if (!deq_args_ok(c, layer, kv_idx, group_start, group_count) ||
+        (group_count > 0 && !out))
+        return eakvi_set_error(EAKV_ERR_INVALID, "dequantize_range: invalid argument");
+    if (group_count == 0) return EAKV_OK;
+    int prev, rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    /* staged through the workspace, at most 64 MiB of f32 per pass */
+    const int64_t per = (int64_t)1 << 18;              /* groups: 64 MiB */
+    const int64_t chunk = group_count < per ? group_count : per;
+    rc = eakvi_work_reserve(c, (size_t)chunk * 256);
+    for (int64_t g = 0; rc == EAKV_OK && g < group_count; g += chunk) {
+        const int64_t n = group_count - g < chunk ? group_count - g : chunk;
+        int e = eakvd_dequantize(&c->geom, c->dev, layer, kv_idx, group_start + g, n,
+                                 (float *)c->work, c->stream);
+        if (!e) e = eakvd_memcpy_d2h_async(out + g * 64, c->work, (size_t)n * 256, c->stream);
+        if (!e) e = eakvd_stream_sync(c->stream);
+        if (e) rc = eakvi_hip_fail(e, "dequantize_range");
+    }
+    eakvi_leave(prev);
+    return rc;
+}
+
+int eakv_validate(const eakv_cache_t *cc, int32_t *results)
+{
+    eakv_cache_t *c = (eakv_cache_t *)cc;
+    if (!c || !results)
+        return eakvi_set_error(EAKV_ERR_INVALID, "validate: invalid argument");
+    const int nb = 2 * c->n_layers;
+    /* the groups the reference checks per block: src/cli.c:49 */
+    const int64_t n = (int64_t)c->n_kv_heads * c->head_dim * c->seq_len / 64;
+    int prev, rc = eakvi_enter(c, &prev);
+    if (rc) return rc;
+    unsigned long long *h = malloc((size_t)nb * sizeof(*h));
+    if (!h) {
+        eakvi_leave(prev);
+        return eakvi_set_error(EAKV_ERR_ALLOC, "validate: out of host memory");
+    }
+    rc = eakvi_work_reserve(c, (size_t)nb * sizeof(*h));
+    if (rc == EAKV_OK) {
+        int e = eakvd_validate(&c->geom, c->dev, nb, n, (unsigned long long *)c->work,
+                               c->stream);
+        if (!e) e = eakvd_memcpy_d2h_async(h, c->work, (size_t)nb * sizeof(*h), c->stream);
+        if (!e) e = eakvd_stream_sync(c->stream);
+        if (e) rc = eakvi_hip_fail(e, "validate");
+    }
+    if (rc == EAKV_OK)
+        for (int i = 0; i < nb; i++) results[i] = h[i] == ~0ull ? 0 : (int32_t)(h[i] & 3);
+    free(h);
+    eakvi_leave(prev);
+    return rc;
+}

@@ -9,7 +9,9 @@
  *     of the same shape (one launch per layer for all sequences);
  *   - the fused single-pass softmax attention, which the reference compiles
  *     (kernels/fused_attention.ea:190-373) but never wires into its C API;
- *   - plane read-back and an error side channel for the void attention calls.
+ *   - plane read-back and an error side channel for the void attention calls;
+ *   - dequantization and the integrity check of GPU-resident planes, which the
+ *     reference runs on its host planes from its benchmark and CLI.
  * Device-pointer calls return when the work is enqueued; results are ready
  * after eakv_cache_sync() or a wait on the stream.
  */
@@ -83,6 +85,29 @@ int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
                                       const float *d_q, int n_q_heads,
                                       int n_kv_heads, float *d_out,
                                       void *stream);
+
+/* Dequantize groups [group_start, group_start + group_count) of the (layer,
+ * kv_idx) planes to f32, 64 values per group in group order: value =
+ * fma(nibble, scale, bias) with byte k of a group holding dim k (low nibble)
+ * and dim k+32 (high nibble).  Group indices are plane indices
+ * (h*max_seq_len*head_dim/64 + t*head_dim/64 + j).  Replaces the reference's
+ * q4_dequantize_range_avx512_f32 (kernels/dequantize_avx512.ea:55-89; the
+ * whole plane, q4_dequantize_avx512_f32, :10-53, is group_start 0 and
+ * group_count n_kv_heads*max_seq_len*head_dim/64).  _device: d_out on the
+ * device, asynchronous on the stream; the other form writes host memory and
+ * returns when done. */
+int eakv_dequantize_range_device(const eakv_cache_t *cache, int layer, int kv_idx,
+                                 int64_t group_start, int64_t group_count,
+                                 float *d_out, void *stream);
+int eakv_dequantize_range(const eakv_cache_t *cache, int layer, int kv_idx,
+                          int64_t group_start, int64_t group_count, float *out);
+
+/* Integrity check of every (layer, kv) block, as the reference's `validate`
+ * command (src/cli.c:39-98) runs q4_validate (kernels/validate.ea:14-71) on
+ * the first n_kv_heads*head_dim*seq_len/64 groups of each block:
+ * results[layer*2 + kv] = 0 (ok), 1 (NaN scale), 2 (NaN bias) or 3 (negative
+ * scale), the code of the block's first failing group.  Synchronous. */
+int eakv_validate(const eakv_cache_t *cache, int32_t *results);
 
 #ifdef __cplusplus
 }

@@ -96,6 +96,33 @@ void orc_dequantize(const uint8_t *weights, const float *scales,
             out[g * 64 + j] = fmaf(nib(weights + g * 32, j), scales[g], biases[g]);
 }
 
+void orc_dequantize_range(const uint8_t *weights, const float *scales,
+                          const float *biases, float *out, int64_t group_start,
+                          int64_t group_count)
+{
+    for (int64_t i = 0; i < group_count; i++) {
+        const int64_t g = group_start + i;
+        for (int j = 0; j < 64; j++)
+            out[i * 64 + j] = fmaf(nib(weights + g * 32, j), scales[g], biases[g]);
+    }
+}
+
+int32_t orc_validate(const float *scales, const float *biases, int64_t n_groups)
+{
+    const int32_t nan_exp = 2139095040;               /* 0x7f800000 */
+    for (int64_t g = 0; g < n_groups; g++) {
+        int32_t sb, bb;
+        memcpy(&sb, scales + g, 4);
+        memcpy(&bb, biases + g, 4);
+        if (sb > nan_exp) return 1;
+        if (sb < 0 && sb > -8388608) return 1;        /* 0xff800001..0xffffffff */
+        if (bb > nan_exp) return 2;
+        if (bb < 0 && bb > -8388608) return 2;
+        if (scales[g] < 0.0f) return 3;
+    }
+    return 0;
+}
+
 /* The reference walks a token in 16-lane chunks c = 0..head_dim/16-1:
  * chunk c covers dims c*16..c*16+15, taken from group c/4, bytes
  * ((c%4)&1)*16..+15, low nibble for c%4 < 2 (fused_k_score.ea:195-227). */

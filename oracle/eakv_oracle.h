@@ -40,6 +40,17 @@ void orc_quantize_split(const float *src, uint8_t *weights, float *scales,
 void orc_dequantize(const uint8_t *weights, const float *scales,
                     const float *biases, float *out, int64_t n_groups);
 
+/* kernels/dequantize_avx512.ea:55-89 (q4_dequantize_range_avx512_f32):
+ * groups [group_start, group_start + group_count) to out[i*64 + j]. */
+void orc_dequantize_range(const uint8_t *weights, const float *scales,
+                          const float *biases, float *out, int64_t group_start,
+                          int64_t group_count);
+
+/* kernels/validate.ea:14-71 (q4_validate): the first failing group's code
+ * over groups 0..n_groups-1 in order, per group 1 = NaN scale, 2 = NaN bias,
+ * 3 = negative scale (NaN tested on the bits), else 0. */
+int32_t orc_validate(const float *scales, const float *biases, int64_t n_groups);
+
 /* 16-lane reduce_add of the reference kernels (tree order above). */
 float orc_reduce16(const float *acc);
 

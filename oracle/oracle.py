@@ -22,6 +22,8 @@ _SIG = {
     "orc_quantize_split": (None, [_vp, _vp, _vp, _vp, _i64]),
     "orc_reduce16": (C.c_float, [_vp]),
     "orc_dequantize": (None, [_vp, _vp, _vp, _vp, _i64]),
+    "orc_dequantize_range": (None, [_vp, _vp, _vp, _vp, _i64, _i64]),
+    "orc_validate": (C.c_int32, [_vp, _vp, _i64]),
     "orc_to_i32": (C.c_int32, [C.c_float]),
     "orc_k_score_mha": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _i64]),
     "orc_k_score_gqa": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _i64]),
@@ -118,6 +120,21 @@ def dequantize(w, s, b):
     out = np.zeros((n, 64), np.float32)
     lib().orc_dequantize(_p(w), _p(_f32(s)), _p(_f32(b)), _p(out), n)
     return out
+
+
+def dequantize_range(w, s, b, group_start, group_count):
+    """Plane groups [group_start, +group_count) -> f32[group_count, 64]."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1, 32)
+    out = np.zeros((group_count, 64), np.float32)
+    lib().orc_dequantize_range(_p(w), _p(_f32(s)), _p(_f32(b)), _p(out), group_start,
+                               group_count)
+    return out
+
+
+def validate(s, b, n_groups):
+    """Integrity code of groups 0..n_groups-1 (0 ok, 1 NaN scale, 2 NaN bias,
+    3 negative scale)."""
+    return int(lib().orc_validate(_p(_f32(s)), _p(_f32(b)), n_groups))
 
 
 def k_score(head_dim, q, w, s, b, seq_len, n_q, n_kv, gph):
@@ -233,6 +250,32 @@ class OracleCache:
                                          C.POINTER(C.c_float)), (ng,)).copy()
         b = np.ctypeslib.as_array(C.cast(L.orc_cache_biases(self.h, layer, kv_idx),
                                          C.POINTER(C.c_float)), (ng,)).copy()
+        return w, s, b
+
+    def validate(self):
+        """Per (layer, kv) block, the code of q4_validate over the first
+        n_kv_heads*head_dim*seq_len/64 groups (reference src/cli.c:39-98)."""
+        L = lib()
+        n = (L.orc_cache_n_heads(self.h) * L.orc_cache_head_dim(self.h) *
+             L.orc_cache_seq_len(self.h)) // 64
+        out = []
+        for layer in range(L.orc_cache_n_layers(self.h)):
+            for kv in range(2):
+                out.append(int(L.orc_validate(L.orc_cache_scales(self.h, layer, kv),
+                                              L.orc_cache_biases(self.h, layer, kv), n)))
+        return np.array(out, np.int32)
+
+    def plane_views(self, layer, kv_idx):
+        """Writable numpy views of the oracle cache's (weights, scales,
+        biases) planes (tests plant values through them)."""
+        L = lib()
+        ng = L.orc_cache_max_groups(self.h)
+        w = np.ctypeslib.as_array(C.cast(L.orc_cache_weights(self.h, layer, kv_idx),
+                                         C.POINTER(C.c_uint8)), (ng, 32))
+        s = np.ctypeslib.as_array(C.cast(L.orc_cache_scales(self.h, layer, kv_idx),
+                                         C.POINTER(C.c_float)), (ng,))
+        b = np.ctypeslib.as_array(C.cast(L.orc_cache_biases(self.h, layer, kv_idx),
+                                         C.POINTER(C.c_float)), (ng,))
         return w, s, b
 
     def save(self, path):

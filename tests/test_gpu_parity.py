@@ -334,3 +334,86 @@ def test_fused_parity_config_distributions(E, rng, d, n_q, n_kv, L):
     assert ok, (err, nbad)
     sa = g.attention_scores(q, 0, n_q, n_kv)
     assert np.array_equal(sa, o.attention_scores(q, 0, n_q, n_kv))
+
+
+# ------------------------------------------------- dequantize range, validate
+
+@pytest.mark.parametrize("nh,d,L,lmax", [(2, 128, 37, 40), (3, 64, 100, 128), (1, 64, 1, 1)])
+def test_dequantize_range_bitexact(E, rng, nh, d, L, lmax):
+    """GPU dequantization of plane ranges equals the oracle's bit for bit
+    (fma(nibble, scale, bias)), host and device forms, including ranges at
+    the plane's ends and ranges over never-written groups."""
+    say("dequantize", nh, d, L, lmax)
+    g, o = loaded(E, rng, nh, d, L, lmax)
+    ng = nh * lmax * d // 64
+    for layer, kv in [(0, 0), (1, 1)]:
+        w, s, b = o.read_planes(layer, kv)
+        for g0, n in [(0, ng), (0, 1), (ng - 1, 1), (ng // 3, ng // 2), (5 % ng, 0)]:
+            got = g.dequantize_range(layer, kv, g0, n)
+            assert np.array_equal(got, O.dequantize_range(w, s, b, g0, n)), (layer, kv, g0, n)
+    from eakv_amd.hipmem import DeviceArray
+    d_out = DeviceArray((ng, 64))
+    assert E.lib().eakv_dequantize_range_device(g.h, 1, 0, 0, ng, d_out.ptr, None) == 0
+    g.sync()
+    w, s, b = o.read_planes(1, 0)
+    assert np.array_equal(d_out.download(), O.dequantize_range(w, s, b, 0, ng))
+    L_ = E.lib()
+    for args in [(2, 0, 0, 1), (0, 2, 0, 1), (0, 0, -1, 1), (0, 0, ng, 1), (0, 0, 0, ng + 1)]:
+        assert L_.eakv_dequantize_range_device(g.h, *args, d_out.ptr, None) == E.EAKV_ERR_INVALID
+    g.free()
+    o.free()
+
+
+def test_validate_matches_oracle(E, rng, tmp_path):
+    """Corrupt values planted in an oracle cache travel through an .eakv file
+    to the GPU; eakv_validate reports the reference's code per block (first
+    failing group of the first n_kv*d*seq_len/64 groups), as the oracle does
+    on the same file (a file's caches have max_seq_len = seq_len, so the
+    plane layout differs from the cache that wrote it), before and after a
+    restore shortens the checked range."""
+    nl, nh, d, L, lmax = 4, 3, 128, 50, 64
+    o = O.OracleCache(nl, nh, d, lmax)
+    o.load_raw(rng.standard_normal((nl, 2, nh, L, d)).astype(np.float32), L)
+    n = nh * d * L // 64
+    plant = {(0, 1): ("s", 7, np.float32(np.nan)),             # 1: NaN scale
+             (1, 0): ("b", n - 1, np.float32(np.nan)),         # 2: NaN bias, last group
+             (2, 0): ("s", 0, np.float32(-3.0)),               # 3: negative scale
+             (2, 1): ("b", n, np.float32(np.nan)),             # beyond the range: ok
+             (3, 1): ("s", 10, np.float32(-np.inf))}           # 3: -inf scale
+    for (layer, kv), (which, gi, v) in plant.items():
+        _, s, b = o.plane_views(layer, kv)
+        (s if which == "s" else b)[gi] = v
+    _, s, b = o.plane_views(3, 1)
+    b[4] = np.float32(np.nan)                                  # earlier group wins: 2
+    assert o.validate().tolist() == [0, 1, 2, 0, 3, 0, 0, 2]
+    path = tmp_path / "planted.eakv"
+    o.save(str(path))
+    g = E.Cache.load(str(path))
+    o2 = O.OracleCache.load(str(path))
+    want = o2.validate()
+    assert want.tolist() == [0, 1, 2, 0, 3, 2, 0, 2]        # (2,1)'s group is in range now
+    assert g.validate().tolist() == want.tolist()
+    for sl in (40, 1, 0):
+        g.restore(sl)
+        o2.restore(sl)
+        assert g.validate().tolist() == o2.validate().tolist(), sl
+    g.free()
+    o.free()
+    o2.free()
+
+
+def test_validate_nan_input_gives_nan_bias(E, rng):
+    """A group whose first value is NaN quantizes to bias NaN (the min scan
+    starts from element 0): validate says 2 on the GPU and in the oracle."""
+    nl, nh, d, L = 1, 2, 64, 8
+    data = rng.standard_normal((nl, 2, nh, L, d)).astype(np.float32)
+    data[0, 1, 1, 3, 0] = np.nan
+    g, o = pair(E, nl, nh, d, L)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    assert o.validate().tolist() == [0, 2]
+    assert g.validate().tolist() == [0, 2]
+    g.clear()
+    assert g.validate().tolist() == [0, 0]                     # no groups checked
+    g.free()
+    o.free()

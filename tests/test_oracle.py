@@ -245,3 +245,76 @@ def test_fused_empty_context_is_nan():
     c = O.OracleCache(1, 1, 64, 8)
     out = c.attention_fused(np.ones((1, 64), np.float32), 0, 1, 1)
     assert np.isnan(out).all()
+
+
+# ------------------------------------------------- dequantize range, validate
+
+def test_dequantize_range_is_a_slice_of_the_closed_form(rng):
+    w = rng.integers(0, 256, (50, 32), dtype=np.uint8)
+    # scales and biases on a 1/16 grid: every n*s + b is exact in f32, so the
+    # closed form needs no rounding
+    s = (rng.integers(-128, 128, 50) / 16).astype(np.float32)
+    b = (rng.integers(-128, 128, 50) / 16).astype(np.float32)
+    # per group: dim j < 32 from the low nibble of byte j, dim j >= 32 from
+    # the high nibble of byte j - 32
+    lo, hi = (w & 15).astype(np.float64), (w >> 4).astype(np.float64)
+    nib = np.concatenate([lo, hi], axis=1)
+    want = (nib * s[:, None].astype(np.float64) + b[:, None]).astype(np.float32)
+    for g0, n in [(0, 50), (7, 13), (49, 1), (20, 0)]:
+        got = O.dequantize_range(w, s, b, g0, n)
+        assert got.shape == (n, 64)
+        assert np.array_equal(got, want[g0:g0 + n])
+
+
+def _bits(u):
+    return np.array([u], np.uint32).view(np.float32)[0]
+
+
+def test_validate_codes_and_first_failure():
+    n = 16
+    ok_s, ok_b = np.full(n, 0.5, np.float32), np.full(n, -1.0, np.float32)
+    assert O.validate(ok_s, ok_b, n) == 0
+    cases = [
+        # (group, scale, bias, code); NaN read from the bits, either sign
+        (3, _bits(0x7fc00000), -1.0, 1),          # quiet NaN scale
+        (3, _bits(0xffc00000), -1.0, 1),          # negative NaN scale
+        (3, _bits(0x7f800001), -1.0, 1),          # signalling NaN scale
+        (5, 0.5, _bits(0x7fc00000), 2),           # NaN bias
+        (5, 0.5, _bits(0xffffffff), 2),           # NaN bias, all bits set
+        (6, -1.0, -1.0, 3),                       # negative scale
+        (6, -np.inf, -1.0, 3),                    # -inf scale: not NaN, negative
+        (6, _bits(0x80000001), -1.0, 3),          # negative denormal scale
+        (9, -0.0, -1.0, 0),                       # -0.0 is not < 0
+        (9, np.inf, np.inf, 0),                   # +inf scale and bias pass
+        (9, 0.5, -np.inf, 0),
+        (2, _bits(0x7fc00000), _bits(0x7fc00000), 1),  # scale checked first
+        (2, -1.0, _bits(0x7fc00000), 2),          # bias NaN before the sign
+    ]
+    for g, sv, bv, code in cases:
+        s, b = ok_s.copy(), ok_b.copy()
+        s[g], b[g] = sv, bv
+        assert O.validate(s, b, n) == code, (g, sv, bv)
+        assert O.validate(s, b, g) == 0           # groups before g only
+    # the first failing group decides, not the lowest code
+    s, b = ok_s.copy(), ok_b.copy()
+    b[3] = np.nan
+    s[5] = -2.0
+    assert O.validate(s, b, n) == 2
+    s, b = ok_s.copy(), ok_b.copy()
+    s[2] = -2.0
+    s[7] = np.nan
+    assert O.validate(s, b, n) == 3
+
+
+def test_validate_cache_covers_the_reference_group_range(rng):
+    nl, nh, d, L, lmax = 2, 3, 64, 5, 8
+    c = O.OracleCache(nl, nh, d, lmax)
+    c.load_raw(rng.standard_normal((nl, 2, nh, L, d)).astype(np.float32), L)
+    assert c.validate().tolist() == [0, 0, 0, 0]
+    n = nh * d * L // 64                          # reference src/cli.c:49
+    _, s, _ = c.plane_views(1, 0)
+    s[n - 1] = -1.0                               # last checked group
+    _, _, b = c.plane_views(0, 1)
+    b[n] = np.nan                                 # first unchecked group
+    assert c.validate().tolist() == [0, 0, 3, 0]
+    c.free()
