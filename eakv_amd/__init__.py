@@ -74,6 +74,10 @@ SIGNATURES = {
         C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp, _vp]),
     "eakv_dequantize_range": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp]),
     "eakv_validate": (C.c_int, [_vp, _vp]),
+    "eakv_ggml_quantize_row_device": (C.c_int, [_vp, _vp, C.c_int64, _vp]),
+    "eakv_ggml_dequantize_row_device": (C.c_int, [_vp, _vp, C.c_int64, _vp]),
+    "eakv_ggml_vec_dot_device": (C.c_int, [C.c_int, _vp, C.c_size_t, _vp, C.c_size_t, _vp,
+                                           C.c_size_t, C.c_int, _vp]),
 }
 
 _LIB = None

@@ -119,6 +119,12 @@ int eakvd_dequantize(const eakvd_geom *g, const uint8_t *base, int layer, int kv
 int eakvd_validate(const eakvd_geom *g, const uint8_t *base, int n_blocks,
                    int64_t n, unsigned long long *res, void *stream);
 
+/* ---- ggml block type (hip/ggml.hip): 40-byte blocks of 64 values */
+int eakvd_ggml_quantize_row(const float *src, void *dst, int64_t k, void *stream);
+int eakvd_ggml_dequantize_row(const void *src, float *dst, int64_t k, void *stream);
+int eakvd_ggml_vec_dot(int n, float *s, size_t bs, const void *vx, size_t bx,
+                       const void *vy, size_t by, int nrc, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

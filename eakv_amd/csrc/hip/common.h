@@ -65,6 +65,61 @@ __device__ __forceinline__ float wave_sum(float v)
 
 static inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
+// ---- Q4 group quantization pieces shared by the cache quantizer and the
+// ggml block type (16 lanes per 64-value group, lane l holding elements
+// 4l..4l+3 as a float4; slot_shift = the group's first lane in the wave).
+
+// f32 -> i32 with x86 cvttss2si semantics (NaN / out of range -> INT32_MIN).
+__device__ __forceinline__ int to_i32_x86(float v)
+{
+    return (v >= -2147483648.0f && v < 2147483648.0f) ? (int)v : (int)0x80000000;
+}
+
+// q(x) = clamp(to_i32((x - mn)*inv + 0.5), 0, 15), each step rounded.
+__device__ __forceinline__ uint32_t q4(float x, float mn, float inv)
+{
+    float v = __fadd_rn(__fmul_rn(__fsub_rn(x, mn), inv), 0.5f);
+    int q = to_i32_x86(v);
+    q = q < 0 ? 0 : (q > 15 ? 15 : q);
+    return (uint32_t)q;
+}
+
+// First element (in index order 4*lane16 + i) of the group that compares
+// equal to zero; its value carries the sign a strict scan keeps.
+__device__ __forceinline__ float first_zero(const float4 &x, int slot_shift)
+{
+    float mine = x.x == 0.0f ? x.x
+               : (x.y == 0.0f ? x.y : (x.z == 0.0f ? x.z : x.w));
+    bool has = (x.x == 0.0f) | (x.y == 0.0f) | (x.z == 0.0f) | (x.w == 0.0f);
+    uint64_t m = __ballot(has);
+    uint32_t sm = (uint32_t)(m >> slot_shift) & 0xffffu;
+    int src = __ffs((int)sm) - 1;
+    if (src < 0) src = 0;
+    return __shfl(mine, src, 16);
+}
+
+// min and max of a group as a strict </> scan from element 0 finds them:
+// the first occurrence wins (so +0 / -0 as they come first), NaN elements
+// after element 0 are skipped, a NaN element 0 gives min = max = NaN.
+__device__ __forceinline__ void group_minmax(const float4 &x, int slot_shift, float &mn,
+                                             float &mx)
+{
+    mn = fminf(fminf(x.x, x.y), fminf(x.z, x.w));
+    mx = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+    }
+    if (mn == 0.0f || mx == 0.0f) {
+        const float z = first_zero(x, slot_shift);
+        if (mn == 0.0f) mn = z;
+        if (mx == 0.0f) mx = z;
+    }
+    const float x0 = __shfl(x.x, 0, 16);
+    if (x0 != x0) { mn = x0; mx = x0; }
+}
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 

@@ -15,40 +15,9 @@
 // Work split: 16 lanes per group, each lane one float4 (elements 4l..4l+3,
 // so lanes 0-7 carry the low-nibble half and lanes 8-15 the high half).
 // A wave covers 4 groups = 1 KB of contiguous f32 per load instruction.
-#include <climits>
-
 #include "common.h"
 
 namespace {
-
-__device__ __forceinline__ int to_i32_x86(float v)
-{
-    return (v >= -2147483648.0f && v < 2147483648.0f) ? (int)v : INT_MIN;
-}
-
-__device__ __forceinline__ uint32_t q4(float x, float mn, float inv)
-{
-    float v = __fadd_rn(__fmul_rn(__fsub_rn(x, mn), inv), 0.5f);
-    int q = to_i32_x86(v);
-    q = q < 0 ? 0 : (q > 15 ? 15 : q);
-    return (uint32_t)q;
-}
-
-// First element (in index order 4*lane16 + i) of the 16-lane slot that
-// compares equal to zero; its value carries the sign the reference keeps.
-__device__ __forceinline__ float first_zero(const float4 &x, int lane16,
-                                            int slot_shift, bool &found)
-{
-    float mine = x.x == 0.0f ? x.x
-               : (x.y == 0.0f ? x.y : (x.z == 0.0f ? x.z : x.w));
-    bool has = (x.x == 0.0f) | (x.y == 0.0f) | (x.z == 0.0f) | (x.w == 0.0f);
-    uint64_t m = __ballot(has);
-    uint32_t sm = (uint32_t)(m >> slot_shift) & 0xffffu;
-    found = sm != 0;
-    int src = __ffs((int)sm) - 1;
-    if (src < 0) src = 0;
-    return __shfl(mine, src, 16);
-}
 
 template <int NT, bool VEC>
 __global__ __launch_bounds__(NT) void quantize_kernel(eakvd_geom g,
@@ -82,22 +51,8 @@ __global__ __launch_bounds__(NT) void quantize_kernel(eakvd_geom g,
                 x.x = xp[0]; x.y = xp[1]; x.z = xp[2]; x.w = xp[3];
             }
 
-            // min/max of non-NaN values; ties between +0 and -0 fixed below.
-            float mn = fminf(fminf(x.x, x.y), fminf(x.z, x.w));
-            float mx = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
-#pragma unroll
-            for (int o = 8; o >= 1; o >>= 1) {
-                mn = fminf(mn, __shfl_xor(mn, o, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, o, 16));
-            }
-            if (mn == 0.0f || mx == 0.0f) {
-                bool found;
-                float z = first_zero(x, lane16, slot_shift, found);
-                if (mn == 0.0f) mn = z;
-                if (mx == 0.0f) mx = z;
-            }
-            const float x0 = __shfl(x.x, 0, 16);
-            if (x0 != x0) { mn = x0; mx = x0; }
+            float mn, mx;
+            group_minmax(x, slot_shift, mn, mx);
 
             const float range = __fsub_rn(mx, mn);
             float scale = 1.0f, inv = 0.0f;

@@ -18,6 +18,7 @@
 #ifndef EAKV_HIP_H
 #define EAKV_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include "eakv.h"
@@ -108,6 +109,24 @@ int eakv_dequantize_range(const eakv_cache_t *cache, int layer, int kv_idx,
  * results[layer*2 + kv] = 0 (ok), 1 (NaN scale), 2 (NaN bias) or 3 (negative
  * scale), the code of the block's first failing group.  Synchronous. */
 int eakv_validate(const eakv_cache_t *cache, int32_t *results);
+
+/* The ggml block type of reference include/eakv_ggml.h:27-31
+ * (block_q4_1_eakv: u8 qs[32] split-packed, f32 d, f32 m; 64 values in 40
+ * bytes), device-pointer forms of its type-trait callbacks for a HIP ggml
+ * backend, on the current HIP device and the given stream (NULL: the
+ * default stream).  Pointers and byte strides are 4-byte aligned.
+ *   _quantize_row:   eakv_quantize_row (src/ggml_type.c:21-90), k values
+ *                    (k % 64 == 0) to k/64 blocks;
+ *   _dequantize_row: eakv_dequantize_row (:96-133), value = fma(n, d, m)
+ *                    (the reference's AVX-512 path; its scalar fallback
+ *                    rounds n*d before adding m);
+ *   _vec_dot:        eakv_vec_dot_q4_f32 (:142-242) for nrc rows of any
+ *                    count: s[r] = row r of vx . row r of vy over n values,
+ *                    the AVX-512 path's 16 lane accumulators and tree. */
+int eakv_ggml_quantize_row_device(const float *d_src, void *d_dst, int64_t k, void *stream);
+int eakv_ggml_dequantize_row_device(const void *d_src, float *d_dst, int64_t k, void *stream);
+int eakv_ggml_vec_dot_device(int n, float *d_s, size_t bs, const void *d_vx, size_t bx,
+                             const void *d_vy, size_t by, int nrc, void *stream);
 
 #ifdef __cplusplus
 }

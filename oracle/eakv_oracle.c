@@ -107,6 +107,72 @@ void orc_dequantize_range(const uint8_t *weights, const float *scales,
     }
 }
 
+void orc_ggml_quantize_row(const float *src, uint8_t *dst, int64_t k)
+{
+    for (int64_t i = 0; i < k / 64; i++) {
+        const float *x = src + i * 64;
+        uint8_t *blk = dst + i * 40;
+        float mn = x[0], mx = x[0];
+        for (int j = 1; j < 64; j++) {
+            if (x[j] < mn) mn = x[j];
+            if (x[j] > mx) mx = x[j];
+        }
+        const float range = mx - mn;
+        const float d = range / 15.0f;
+        const float id = range > 0.0f ? 15.0f / range : 0.0f;
+        memcpy(blk + 32, &d, 4);
+        memcpy(blk + 36, &mn, 4);
+        for (int j = 0; j < 32; j++) {
+            int lo = (int)(0.5f + (x[j] - mn) * id);
+            int hi = (int)(0.5f + (x[j + 32] - mn) * id);
+            lo = lo < 0 ? 0 : lo > 15 ? 15 : lo;
+            hi = hi < 0 ? 0 : hi > 15 ? 15 : hi;
+            blk[j] = (uint8_t)(lo | (hi << 4));
+        }
+    }
+}
+
+void orc_ggml_dequantize_row(const uint8_t *src, float *dst, int64_t k)
+{
+    for (int64_t i = 0; i < k / 64; i++) {
+        const uint8_t *blk = src + i * 40;
+        float d, m;
+        memcpy(&d, blk + 32, 4);
+        memcpy(&m, blk + 36, 4);
+        for (int j = 0; j < 32; j++) {
+            dst[i * 64 + j] = fmaf((float)(blk[j] & 15), d, m);
+            dst[i * 64 + j + 32] = fmaf((float)(blk[j] >> 4), d, m);
+        }
+    }
+}
+
+void orc_ggml_vec_dot(int n, float *s, size_t bs, const uint8_t *vx, size_t bx,
+                      const float *vy, size_t by, int nrc)
+{
+    for (int r = 0; r < nrc; r++) {
+        const uint8_t *x = vx + r * bx;
+        const float *y = (const float *)((const char *)vy + r * by);
+        float acc[16] = {0};
+        for (int i = 0; i < n / 64; i++) {
+            const uint8_t *blk = x + (int64_t)i * 40;
+            float d, m;
+            memcpy(&d, blk + 32, 4);
+            memcpy(&m, blk + 36, 4);
+            for (int c = 0; c < 2; c++) {
+                for (int l = 0; l < 16; l++) {
+                    const float v = fmaf((float)(blk[c * 16 + l] & 15), d, m);
+                    acc[l] = fmaf(v, y[i * 64 + c * 16 + l], acc[l]);
+                }
+                for (int l = 0; l < 16; l++) {
+                    const float v = fmaf((float)(blk[c * 16 + l] >> 4), d, m);
+                    acc[l] = fmaf(v, y[i * 64 + c * 16 + 32 + l], acc[l]);
+                }
+            }
+        }
+        *(float *)((char *)s + r * bs) = orc_reduce16(acc);
+    }
+}
+
 int32_t orc_validate(const float *scales, const float *biases, int64_t n_groups)
 {
     const int32_t nan_exp = 2139095040;               /* 0x7f800000 */

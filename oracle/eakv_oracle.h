@@ -51,6 +51,21 @@ void orc_dequantize_range(const uint8_t *weights, const float *scales,
  * 3 = negative scale (NaN tested on the bits), else 0. */
 int32_t orc_validate(const float *scales, const float *biases, int64_t n_groups);
 
+/* ---- ggml block type (reference include/eakv_ggml.h:27-31): 40-byte
+ * blocks {u8 qs[32] split-packed, f32 d, f32 m} of 64 values.
+ * orc_ggml_quantize_row: src/ggml_type.c:21-87 (min/max scan from element 0,
+ * d = range/15, id = range > 0 ? 15/range : 0, q = clamp(trunc(0.5 +
+ * (x - min)*id), 0, 15); the AVX-512 and scalar paths agree on finite
+ * input).  orc_ggml_dequantize_row: ggml_type.c:96-133, the AVX-512 path,
+ * value = fma(nibble, d, m).  orc_ggml_vec_dot: ggml_type.c:142-242, the
+ * AVX-512 path: 16 lane accumulators, per block for c = 0, 1 the low then
+ * the high nibbles, acc = fma(fma(n, d, m), y, acc), then the lanes summed
+ * by the tree of orc_reduce16; rows r < nrc at byte strides bs, bx, by. */
+void orc_ggml_quantize_row(const float *src, uint8_t *dst, int64_t k);
+void orc_ggml_dequantize_row(const uint8_t *src, float *dst, int64_t k);
+void orc_ggml_vec_dot(int n, float *s, size_t bs, const uint8_t *vx, size_t bx,
+                      const float *vy, size_t by, int nrc);
+
 /* 16-lane reduce_add of the reference kernels (tree order above). */
 float orc_reduce16(const float *acc);
 

@@ -14,6 +14,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_LIB_PATH = os.path.join(HERE, "_ref", "libggml_ref.so")
+REF_AVX512_PATH = os.path.join(HERE, "_ref", "libggml_ref_avx512.so")
 
 _vp = C.c_void_p
 _i64 = C.c_int64
@@ -24,6 +25,10 @@ _SIG = {
     "orc_dequantize": (None, [_vp, _vp, _vp, _vp, _i64]),
     "orc_dequantize_range": (None, [_vp, _vp, _vp, _vp, _i64, _i64]),
     "orc_validate": (C.c_int32, [_vp, _vp, _i64]),
+    "orc_ggml_quantize_row": (None, [_vp, _vp, _i64]),
+    "orc_ggml_dequantize_row": (None, [_vp, _vp, _i64]),
+    "orc_ggml_vec_dot": (None, [C.c_int, _vp, C.c_size_t, _vp, C.c_size_t, _vp, C.c_size_t,
+                                C.c_int]),
     "orc_to_i32": (C.c_int32, [C.c_float]),
     "orc_k_score_mha": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, _i64]),
     "orc_k_score_gqa": (None, [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _i64]),
@@ -74,21 +79,40 @@ def lib():
     return _LIB
 
 
-def ref_lib():
-    """The reference's own src/ggml_type.c, built by `make -C oracle ref`
-    (None when it was not built: only where the reference sources exist)."""
-    global _REF
+def _cpu_has_avx512():
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        return False
+    return all(f in flags for f in ("avx512f", "avx512bw", "avx512vl", "avx512dq"))
+
+
+_REF_AVX = None
+
+
+def ref_lib(avx512=False):
+    """The reference's own src/ggml_type.c, built by `make -C oracle ref`:
+    its scalar paths, or (avx512=True) its AVX-512 paths, the latter only on
+    a CPU with AVX-512 (None when not built or not runnable)."""
+    global _REF, _REF_AVX
+    if avx512:
+        if _REF_AVX is None and os.path.exists(REF_AVX512_PATH) and _cpu_has_avx512():
+            _REF_AVX = _bind_ref(C.CDLL(REF_AVX512_PATH))
+        return _REF_AVX
     if _REF is None and os.path.exists(REF_LIB_PATH):
-        h = C.CDLL(REF_LIB_PATH)
-        h.eakv_quantize_row.restype = None
-        h.eakv_quantize_row.argtypes = [_vp, _vp, C.c_int64]
-        h.eakv_dequantize_row.restype = None
-        h.eakv_dequantize_row.argtypes = [_vp, _vp, C.c_int64]
-        h.eakv_vec_dot_q4_f32.restype = None
-        h.eakv_vec_dot_q4_f32.argtypes = [C.c_int, _vp, C.c_size_t, _vp, C.c_size_t,
-                                          _vp, C.c_size_t, C.c_int]
-        _REF = h
+        _REF = _bind_ref(C.CDLL(REF_LIB_PATH))
     return _REF
+
+
+def _bind_ref(h):
+    h.eakv_quantize_row.restype = None
+    h.eakv_quantize_row.argtypes = [_vp, _vp, C.c_int64]
+    h.eakv_dequantize_row.restype = None
+    h.eakv_dequantize_row.argtypes = [_vp, _vp, C.c_int64]
+    h.eakv_vec_dot_q4_f32.restype = None
+    h.eakv_vec_dot_q4_f32.argtypes = [C.c_int, _vp, C.c_size_t, _vp, C.c_size_t,
+                                      _vp, C.c_size_t, C.c_int]
+    return h
 
 
 def _p(a):
@@ -135,6 +159,32 @@ def validate(s, b, n_groups):
     """Integrity code of groups 0..n_groups-1 (0 ok, 1 NaN scale, 2 NaN bias,
     3 negative scale)."""
     return int(lib().orc_validate(_p(_f32(s)), _p(_f32(b)), n_groups))
+
+
+def ggml_quantize_row(x):
+    """f32[k] (k % 64 == 0) -> u8[k/64, 40] blocks (qs[32], d, m)."""
+    x = _f32(x).reshape(-1)
+    out = np.zeros((x.size // 64, 40), np.uint8)
+    lib().orc_ggml_quantize_row(_p(x), _p(out), x.size)
+    return out
+
+
+def ggml_dequantize_row(blocks):
+    """u8[nb, 40] blocks -> f32[nb*64]."""
+    blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1, 40)
+    out = np.zeros(blocks.shape[0] * 64, np.float32)
+    lib().orc_ggml_dequantize_row(_p(blocks), _p(out), out.size)
+    return out
+
+
+def ggml_vec_dot(blocks, y):
+    """Row r of blocks (u8[nrc, nb*40]) dotted with row r of y (f32[nrc, nb*64])."""
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    y = _f32(y)
+    nrc, n = y.shape
+    s = np.zeros(nrc, np.float32)
+    lib().orc_ggml_vec_dot(n, _p(s), 4, _p(blocks), blocks.shape[1], _p(y), n * 4, nrc)
+    return s
 
 
 def k_score(head_dim, q, w, s, b, seq_len, n_q, n_kv, gph):

@@ -1,4 +1,5 @@
-"""Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
+"""Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py
+and, for the ggml block type, tests/golden/make_ggml_golden.py).
 
 The fixtures hold seeded inputs and the expected quantized planes, K-scores,
 softmax weights, V-sums and fused outputs.  The CPU tests pin the oracle to
@@ -31,7 +32,7 @@ def bits(a):
 
 def test_manifest_sha256():
     manifest = json.load(open(os.path.join(GOLD, "manifest.json")))
-    assert sorted(manifest) == sorted([n + ".npz" for n in ["special_groups"] + ATTN])
+    assert sorted(manifest) == sorted([n + ".npz" for n in ["special_groups", "ggml_rows"] + ATTN])
     for fname, digest in manifest.items():
         got = hashlib.sha256(open(os.path.join(GOLD, fname), "rb").read()).hexdigest()
         assert got == digest, fname
@@ -144,3 +145,45 @@ def test_gpu_fixture_parity(name):
         fused = c.attention_fused(f["q"], 0, n_q, n_kv)
         ok, err, nbad = tol_close(fused, f["fused"])
         assert ok, (err, nbad)
+
+
+# ------------------------------------------------------- ggml block type
+
+def test_oracle_reproduces_ggml_fixture():
+    """The fixture's values come from the reference's ggml_type.c (scalar
+    quantizer, AVX-512 dequantize and vec_dot); the oracle matches them."""
+    import oracle as O
+    g = load("ggml_rows")
+    assert np.array_equal(O.ggml_quantize_row(g["x"]), g["blocks"])
+    assert np.array_equal(bits(O.ggml_dequantize_row(g["blocks"])), bits(g["deq"]))
+    assert np.array_equal(bits(O.ggml_vec_dot(g["dot_x"], g["dot_y"])), bits(g["dot"]))
+    # closed forms: a constant block stores d = 0 (no range check, unlike the
+    # cache quantizer's scale 1), m = the value, nibbles 0
+    blk = g["blocks"][0]
+    assert blk[32:36].view(np.float32)[0] == 0.0 and not blk[:32].any()
+    assert blk[36:40].view(np.float32)[0] == np.float32(3.25)
+    # 0..63: d = 63/15, m = 0, element 0 -> 0 and element 63 -> 15
+    blk = g["blocks"][1]
+    assert blk[32:36].view(np.float32)[0] == np.float32(63.0) / np.float32(15.0)
+    assert (blk[0] & 15) == 0 and (blk[31] >> 4) == 15
+
+
+@pytest.mark.gpu
+def test_gpu_ggml_fixture_bit_exact():
+    import eakv_amd as E
+    from eakv_amd.hipmem import DeviceArray
+    g = load("ggml_rows")
+    L = E.lib()
+    dx = DeviceArray.from_host(g["x"])
+    db = DeviceArray((g["blocks"].size,), np.uint8)
+    assert L.eakv_ggml_quantize_row_device(dx.ptr, db.ptr, g["x"].size, None) == 0
+    dd = DeviceArray((g["x"].size,))
+    assert L.eakv_ggml_dequantize_row_device(db.ptr, dd.ptr, g["x"].size, None) == 0
+    dvx, dvy = DeviceArray.from_host(g["dot_x"]), DeviceArray.from_host(g["dot_y"])
+    ds = DeviceArray((3,))
+    n = g["dot_y"].shape[1]
+    assert L.eakv_ggml_vec_dot_device(n, ds.ptr, 4, dvx.ptr, g["dot_x"].shape[1], dvy.ptr,
+                                      n * 4, 3, None) == 0
+    assert np.array_equal(db.download().reshape(-1, 40), g["blocks"])
+    assert np.array_equal(bits(dd.download()), bits(g["deq"]))
+    assert np.array_equal(bits(ds.download()), bits(g["dot"]))

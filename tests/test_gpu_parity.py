@@ -417,3 +417,56 @@ def test_validate_nan_input_gives_nan_bias(E, rng):
     assert g.validate().tolist() == [0, 0]                     # no groups checked
     g.free()
     o.free()
+
+
+# -------------------------------------------------------- ggml block type
+
+@pytest.mark.parametrize("nb,nrc,off", [(1, 1, 0), (333, 5, 0), (4096, 2, 4), (17, 64, 4)])
+def test_ggml_rows_bitexact(E, rng, nb, nrc, off):
+    """eakv_ggml_* against the oracle's restatement of ggml_type.c, bit for
+    bit: quantize (scalar-path min/max), dequantize and vec_dot (AVX-512
+    path arithmetic), with 4-byte (not 16-byte) aligned buffers when off = 4,
+    a shared f32 row (by = 0) and several rows per call."""
+    from eakv_amd.hipmem import DeviceArray
+    say("ggml", nb, nrc, off)
+    L = E.lib()
+    x = (rng.standard_normal(nb * 64) * np.exp(rng.uniform(-5, 5))).astype(np.float32)
+    x[rng.integers(0, x.size, 3)] = 0.0
+    pad = off // 4
+    dx = DeviceArray.from_host(np.concatenate([np.zeros(pad, np.float32), x]))
+    db = DeviceArray((nb * 40 + off,), np.uint8)
+    assert L.eakv_ggml_quantize_row_device(dx.ptr + off, db.ptr + off, x.size, None) == 0
+    dd = DeviceArray((x.size + pad,))
+    assert L.eakv_ggml_dequantize_row_device(db.ptr + off, dd.ptr + off, x.size, None) == 0
+    E.hipmem.synchronize()
+    blocks = db.download()[off:].reshape(nb, 40)
+    assert np.array_equal(blocks, O.ggml_quantize_row(x))
+    assert np.array_equal(dd.download()[pad:].view(np.uint32),
+                          O.ggml_dequantize_row(blocks).view(np.uint32))
+    n = nb * 64
+    vx = np.stack([O.ggml_quantize_row(rng.standard_normal(n).astype(np.float32)).reshape(-1)
+                   for _ in range(nrc)])
+    vy = rng.standard_normal((nrc, n)).astype(np.float32)
+    dvx, dvy = DeviceArray.from_host(vx), DeviceArray.from_host(vy)
+    ds = DeviceArray((nrc,))
+    assert L.eakv_ggml_vec_dot_device(n, ds.ptr, 4, dvx.ptr, vx.shape[1], dvy.ptr, n * 4, nrc,
+                                      None) == 0
+    ds0 = DeviceArray((nrc,))
+    assert L.eakv_ggml_vec_dot_device(n, ds0.ptr, 4, dvx.ptr, vx.shape[1], dvy.ptr, 0, nrc,
+                                      None) == 0
+    E.hipmem.synchronize()
+    assert np.array_equal(ds.download().view(np.uint32), O.ggml_vec_dot(vx, vy).view(np.uint32))
+    shared = O.ggml_vec_dot(vx, np.repeat(vy[:1], nrc, axis=0))
+    assert np.array_equal(ds0.download().view(np.uint32), shared.view(np.uint32))
+
+
+def test_ggml_rejects_bad_arguments(E):
+    from eakv_amd.hipmem import DeviceArray
+    L = E.lib()
+    d = DeviceArray((1024,))
+    assert L.eakv_ggml_quantize_row_device(d.ptr, d.ptr + 2048, 100, None) == E.EAKV_ERR_INVALID
+    assert L.eakv_ggml_quantize_row_device(d.ptr + 2, d.ptr + 2048, 64, None) == E.EAKV_ERR_INVALID
+    assert L.eakv_ggml_dequantize_row_device(d.ptr, d.ptr + 1, 64, None) == E.EAKV_ERR_INVALID
+    assert L.eakv_ggml_vec_dot_device(64, d.ptr, 2, d.ptr, 40, d.ptr, 256, 2,
+                                      None) == E.EAKV_ERR_INVALID
+    assert L.eakv_ggml_quantize_row_device(None, None, 0, None) == 0

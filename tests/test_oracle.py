@@ -318,3 +318,43 @@ def test_validate_cache_covers_the_reference_group_range(rng):
     b[n] = np.nan                                 # first unchecked group
     assert c.validate().tolist() == [0, 0, 3, 0]
     c.free()
+
+
+# ----------------------------------------------------------- ggml block type
+
+@pytest.mark.parametrize("kind", ["normal", "scaled", "ints"])
+def test_ggml_oracle_matches_reference_builds(rng, kind):
+    """orc_ggml_*: the quantizer equals the reference's ggml_type.c (scalar
+    build) bit for bit; dequantize and vec_dot equal its AVX-512 build bit for
+    bit where the CPU runs it, and its scalar build (unfused n*d + m, one
+    sequential sum) within the scores bar."""
+    S, A = O.ref_lib(), O.ref_lib(avx512=True)
+    if S is None:
+        pytest.skip("oracle/_ref not built (needs the reference sources)")
+    vp = lambda a: a.ctypes.data_as(C.c_void_p)
+    x = _groups(rng, 40, kind).reshape(-1)
+    blk = np.zeros((40, 40), np.uint8)
+    S.eakv_quantize_row(vp(x), vp(blk), x.size)
+    assert np.array_equal(O.ggml_quantize_row(x), blk)
+    n, nrc = 640, 4
+    vx = np.stack([O.ggml_quantize_row(_groups(rng, n // 64, kind).reshape(-1)).reshape(-1)
+                   for _ in range(nrc)])
+    vy = rng.standard_normal((nrc, n)).astype(np.float32)
+    libs = [(S, False)] + ([(A, True)] if A is not None else [])
+    for R, exact in libs:
+        deq = np.zeros(x.size, np.float32)
+        R.eakv_dequantize_row(vp(blk), vp(deq), x.size)
+        dot = np.zeros(nrc, np.float32)
+        R.eakv_vec_dot_q4_f32(n, vp(dot), 4, vp(vx), vx.shape[1], vp(vy), n * 4, nrc)
+        od, ot = O.ggml_dequantize_row(blk), O.ggml_vec_dot(vx, vy)
+        if exact:
+            assert np.array_equal(od.view(np.uint32), deq.view(np.uint32))
+            assert np.array_equal(ot.view(np.uint32), dot.view(np.uint32))
+        else:
+            ok, err, _ = tol_close(od, deq, 1e-4, 1e-5)
+            assert ok, err
+            # two f32 sums of the same n products in different orders: each
+            # within n * 2^-24 * sum|terms| of the exact dot
+            terms = np.stack([O.ggml_dequantize_row(r) for r in vx]).astype(np.float64) * vy
+            bound = 2 * n * 2.0 ** -24 * np.abs(terms).sum(axis=1)
+            assert np.all(np.abs(ot.astype(np.float64) - dot) <= bound)
