@@ -330,6 +330,55 @@ def dequant_bench(w, steps, warmup):
                          "alg_bytes_per_launch": alg}}
 
 
+def unfused_bench(w, steps, warmup):
+    """The reference API's unfused path on the first cache, every layer back
+    to back: eakv_attention_scores_device (k_score_kernel), then
+    eakv_attention_output_device (v_sum_kernel + chunk_sum_kernel) with
+    uniform weights 1/L (timing only; parity is the tests' job).  Returns the
+    JSON line with each call's mean time and GB/s of its algorithmic bytes:
+    K-score n_kv*L*gpd*40 + n_q*L*4 (scores) + n_q*d*4, V-sum
+    n_kv*L*gpd*40 + n_q*L*4 (weights) + n_q*d*4."""
+    E, H, c = w.E, w.H, w.cfg
+    cache = w.caches[0]
+    L = w.L0
+    nq, nkv, d = c["nq"], c["nkv"], c["d"]
+    scores = H.DeviceArray((nq, L))
+    wts = H.DeviceArray.from_host(np.full((nq, L), 1.0 / L, np.float32))
+    out = H.DeviceArray((nq, d))
+    lib = E.lib()
+
+    def run(which):
+        for l in range(c["nl"]):
+            q = w.ql[l].ptr                        # sequence 0's queries
+            if which == "k":
+                rc = lib.eakv_attention_scores_device(cache.h, q, l, nq, nkv, scores.ptr, None)
+            else:
+                rc = lib.eakv_attention_output_device(cache.h, wts.ptr, l, nq, nkv, out.ptr, None)
+            assert rc == 0, E.last_error()
+
+    res = {}
+    alg = nkv * L * (d // 64) * 40 + nq * L * 4 + nq * d * 4
+    for which, name in (("k", "k_score"), ("v", "v_sum")):
+        for _ in range(warmup):
+            run(which)
+        H.synchronize()
+        e0, e1 = H.Event(), H.Event()
+        e0.record(w.stream)
+        for _ in range(steps):
+            run(which)
+        e1.record(w.stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (steps * c["nl"])
+        res[name] = {"us_per_call": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
+                     "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "alg_bytes_per_call": alg}
+    return {"metric": "unfused K-score / V-sum per layer call, GB/s of algorithmic bytes",
+            "unit": "GB/s", "n_gpus": 1, "steps": steps, "dtype": "q4_1 (u8 nibbles + f32 scale/bias), f32 math",
+            "config": {"workload": c["name"], "layers": c["nl"], "q_heads": nq, "kv_heads": nkv,
+                       "head_dim": d, "context": L, "sequences": 1},
+            **res}
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -348,6 +397,9 @@ def main():
     ap.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
     ap.add_argument("--ctx", type=int, default=None, help="override context length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--unfused", action="store_true",
+                    help="only time the unfused K-score and V-sum calls on the first "
+                         "cache, print their JSON line, then exit")
     ap.add_argument("--dequant", action="store_true",
                     help="only time whole-plane dequantization of the first cache, "
                          "print its JSON line, then exit")
@@ -373,6 +425,9 @@ def main():
     H.synchronize()
     if args.dequant:
         print(json.dumps(dequant_bench(w, max(1, args.steps // 4), 1)), flush=True)
+        return
+    if args.unfused:
+        print(json.dumps(unfused_bench(w, max(1, args.steps // 4), 1)), flush=True)
         return
     log(f"bench: quantize {w.quant_bytes / 1e9:.2f} GB alg in {w.quant_ms:.2f} ms "
         f"({w.quant_bytes / w.quant_ms / 1e6:.0f} GB/s)")

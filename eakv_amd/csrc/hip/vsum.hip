@@ -12,19 +12,24 @@
 // Layout: a lane owns one packed dword of a token (8 dims: 4 low nibbles and
 // the 4 high nibbles 32 dims further), D/8 lanes per token, 256/(D/8) token
 // slots per block.  V is dequantized once per token and reused by every q
-// head of its group (at most 8 per pass).
+// head of its group (HP per pass: 1, 2, 4 or 8, the smallest that covers
+// the group up to 8, so registers are spent only on heads that exist).  A lane takes kBatch tokens of its
+// slot at a time and issues all their loads (V word, scale, bias, weights)
+// before the arithmetic, so kBatch loads per lane are in flight; a block
+// covers a chunk of kChunk tokens of one kv head and writes one partial per
+// q head, which chunk_sum_kernel adds in chunk order.
 #include "common.h"
 
 namespace {
 
-constexpr int kHeadsPerPass = 8;
+constexpr int kBatch = 8;
+constexpr int kChunk = 256;
 
-template <int D>
+template <int D, int HP>
 __global__ __launch_bounds__(256) void v_sum_kernel(
     const uint8_t *__restrict__ vw, const float *__restrict__ vs,
     const float *__restrict__ vb, int64_t gph, int L,
-    const float *__restrict__ w, int n_q, int qpk, int chunk,
-    float *__restrict__ partial)
+    const float *__restrict__ w, int n_q, int qpk, float *__restrict__ partial)
 {
     constexpr int GPD = D / 64;
     constexpr int LPT = D / 8;
@@ -36,38 +41,51 @@ __global__ __launch_bounds__(256) void v_sum_kernel(
     const int lt = threadIdx.x % LPT;
     const int slot = threadIdx.x / LPT;
     const int grp = lt / 8, dj = lt % 8;
-    const int t_begin = ch * chunk;
-    const int t_end = min(L, t_begin + chunk);
+    const int t_begin = ch * kChunk;
+    const int t_end = min(L, t_begin + kChunk);
     // dims of this lane: lo e -> 64*grp + 4*dj + e, hi e -> +32
     const int dim_lo = 64 * grp + 4 * dj;
 
-    for (int hb = 0; hb < qpk; hb += kHeadsPerPass) {
-        const int nh = min(kHeadsPerPass, qpk - hb);
-        float acc[kHeadsPerPass][8];
+    for (int hb = 0; hb < qpk; hb += HP) {
+        const int nh = min(HP, qpk - hb);
+        const float *wq = w + (int64_t)(kvh * qpk + hb) * L;
+        float acc[HP][8];
 #pragma unroll
-        for (int o = 0; o < kHeadsPerPass; o++)
+        for (int o = 0; o < HP; o++)
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[o][e] = 0.0f;
 
-        for (int t = t_begin + slot; t < t_end; t += SLOTS) {
-            const int64_t g = (int64_t)kvh * gph + (int64_t)t * GPD + grp;
-            const uint32_t word =
-                *reinterpret_cast<const uint32_t *>(vw + g * 32 + dj * 4);
-            const float s = vs[g], b = vb[g];
-            float v[8];
+        for (int t0 = t_begin + slot; t0 < t_end; t0 += SLOTS * kBatch) {
+            uint32_t word[kBatch];
+            float sc[kBatch], bi[kBatch], wt[kBatch][HP];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                v[e] = fmaf((float)((word >> (8 * e)) & 15u), s, b);
-                v[4 + e] = fmaf((float)((word >> (8 * e + 4)) & 15u), s, b);
+            for (int u = 0; u < kBatch; u++) {
+                const int t = t0 + u * SLOTS;
+                const bool in = t < t_end;
+                const int tt = in ? t : t_begin;
+                const int64_t g = (int64_t)kvh * gph + (int64_t)tt * GPD + grp;
+                word[u] = *reinterpret_cast<const uint32_t *>(vw + g * 32 + dj * 4);
+                sc[u] = vs[g];
+                bi[u] = vb[g];
+#pragma unroll
+                for (int o = 0; o < HP; o++)
+                    wt[u][o] = (in && o < nh) ? wq[(int64_t)o * L + tt] : 0.0f;
             }
 #pragma unroll
-            for (int o = 0; o < kHeadsPerPass; o++) {
-                if (o < nh) {
-                    const int qh = kvh * qpk + hb + o;
-                    const float wt = w[(int64_t)qh * L + t];
+            for (int u = 0; u < kBatch; u++) {
+                if (t0 + u * SLOTS >= t_end) break;
+                float v[8];
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        acc[o][e] = fmaf(v[e], wt, acc[o][e]);
+                for (int e = 0; e < 4; e++) {
+                    v[e] = fmaf((float)((word[u] >> (8 * e)) & 15u), sc[u], bi[u]);
+                    v[4 + e] = fmaf((float)((word[u] >> (8 * e + 4)) & 15u), sc[u], bi[u]);
+                }
+#pragma unroll
+                for (int o = 0; o < HP; o++) {
+                    if (o < nh) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[o][e] = fmaf(v[e], wt[u][o], acc[o][e]);
+                    }
                 }
             }
         }
@@ -75,7 +93,7 @@ __global__ __launch_bounds__(256) void v_sum_kernel(
         // o is unrolled so acc stays in registers; nh is block-uniform, so
         // the barriers below are reached by every thread or by none.
 #pragma unroll
-        for (int o = 0; o < kHeadsPerPass; o++) {
+        for (int o = 0; o < HP; o++) {
             if (o >= nh) break;
             float *r = red + slot * D;
 #pragma unroll
@@ -96,7 +114,8 @@ __global__ __launch_bounds__(256) void v_sum_kernel(
     }
 }
 
-// out[i] = sum over chunks in order of partial[c][i]
+// out[i] = sum over chunks in order of partial[c][i], the chunks read 8 at
+// a time with their loads in flight
 __global__ __launch_bounds__(256) void chunk_sum_kernel(
     const float *__restrict__ partial, int n_chunks, int64_t n_out,
     float *__restrict__ out)
@@ -104,18 +123,16 @@ __global__ __launch_bounds__(256) void chunk_sum_kernel(
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n_out) return;
     float sum = partial[i];
-    for (int c = 1; c < n_chunks; c++)
-        sum = __fadd_rn(sum, partial[(int64_t)c * n_out + i]);
+    for (int c0 = 1; c0 < n_chunks; c0 += 8) {
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            p[j] = c0 + j < n_chunks ? partial[(int64_t)(c0 + j) * n_out + i] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (c0 + j < n_chunks) sum = __fadd_rn(sum, p[j]);
+    }
     out[i] = sum;
-}
-
-int v_sum_chunk(int seq_len, int n_kv)
-{
-    // about 2048 blocks over the kv heads, at least 64 tokens per block
-    int64_t c = ((int64_t)seq_len * n_kv + 2047) / 2048;
-    c = (c + 63) / 64 * 64;
-    if (c < 64) c = 64;
-    return (int)c;
 }
 
 }  // namespace
@@ -124,8 +141,7 @@ extern "C" size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len,
                                          int n_q)
 {
     if (seq_len <= 0) return 0;
-    const int chunk = v_sum_chunk(seq_len, g->n_kv_heads);
-    const int n_chunks = ceil_div_i(seq_len, chunk);
+    const int n_chunks = ceil_div_i(seq_len, kChunk);
     return (size_t)n_chunks * n_q * g->head_dim * sizeof(float);
 }
 
@@ -138,20 +154,17 @@ extern "C" int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base,
     if (seq_len <= 0)
         return (int)hipMemsetAsync(out, 0, n_out * sizeof(float), st);
     const Planes p = planes_of(*g, base, layer, 1);
-    // the chunk is sized from the cache's head count so that the work size
-    // does not depend on n_kv
-    const int chunk = v_sum_chunk(seq_len, g->n_kv_heads);
-    const int n_chunks = ceil_div_i(seq_len, chunk);
+    const int n_chunks = ceil_div_i(seq_len, kChunk);
     const int qpk = n_q / n_kv;
     float *partial = (float *)work;
     const dim3 grid((unsigned)n_chunks, (unsigned)n_kv);
-    if (g->head_dim == 64)
-        hipLaunchKernelGGL(v_sum_kernel<64>, grid, dim3(256), 0, st, p.w, p.s,
-                           p.b, g->gph, seq_len, w, n_q, qpk, chunk, partial);
-    else
-        hipLaunchKernelGGL(v_sum_kernel<128>, grid, dim3(256), 0, st, p.w,
-                           p.s, p.b, g->gph, seq_len, w, n_q, qpk, chunk,
-                           partial);
+    auto kern = g->head_dim == 64
+                    ? (qpk <= 1 ? v_sum_kernel<64, 1> : qpk <= 2 ? v_sum_kernel<64, 2>
+                       : qpk <= 4 ? v_sum_kernel<64, 4> : v_sum_kernel<64, 8>)
+                    : (qpk <= 1 ? v_sum_kernel<128, 1> : qpk <= 2 ? v_sum_kernel<128, 2>
+                       : qpk <= 4 ? v_sum_kernel<128, 4> : v_sum_kernel<128, 8>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, p.w, p.s, p.b, g->gph, seq_len, w, n_q,
+                       qpk, partial);
     hipLaunchKernelGGL(chunk_sum_kernel, dim3((unsigned)ceil_div_i(n_out, 256)),
                        dim3(256), 0, st, partial, n_chunks, n_out, out);
     return (int)hipGetLastError();
