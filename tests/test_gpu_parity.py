@@ -470,3 +470,44 @@ def test_ggml_rejects_bad_arguments(E):
     assert L.eakv_ggml_vec_dot_device(64, d.ptr, 2, d.ptr, 40, d.ptr, 256, 2,
                                       None) == E.EAKV_ERR_INVALID
     assert L.eakv_ggml_quantize_row_device(None, None, 0, None) == 0
+
+
+# ----------------------------------------------------------------- full size
+
+@pytest.mark.parametrize("n_kv,n_q,L", [(8, 32, 32768), (2, 16, 131072)])
+def test_fused_full_size_matches_oracle(E, n_kv, n_q, L):
+    """The benchmark's context lengths: one sequence of the 32Q/8KV 32K
+    workload, and 131072 tokens at 8 q heads per kv head (the 64Q/8KV
+    workload's ratio and length, 2 of its 8 kv heads), against the oracle."""
+    say("fused-full", n_kv, n_q, L)
+    rng = np.random.default_rng(L + n_kv)
+    data = rng.standard_normal((1, 2, n_kv, L, 128), dtype=np.float32)
+    g, o = pair(E, 1, n_kv, 128, L)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    del data
+    q = rng.standard_normal((n_q, 128), dtype=np.float32)
+    ok, err, nbad = tol_close(g.attention_fused(q, 0, n_q, n_kv),
+                              o.attention_fused(q, 0, n_q, n_kv), ATOL, RTOL)
+    assert ok, (err, nbad)
+    g.free()
+    o.free()
+
+
+def test_fused_full_size_zero_query_is_mean_of_v(E):
+    """q = 0 gives every token the same score, so the output is the mean of
+    the dequantized V rows over all 131072 tokens (f64 reference from the
+    cache's own planes)."""
+    n_kv, n_q, L, d = 2, 16, 131072, 128
+    rng = np.random.default_rng(7)
+    data = (rng.standard_normal((1, 2, n_kv, L, d), dtype=np.float32) * 3).astype(np.float32)
+    g = E.Cache(1, n_kv, d, L)
+    g.load_raw(data, L)
+    del data
+    out = g.attention_fused(np.zeros((n_q, d), np.float32), 0, n_q, n_kv)
+    vw, vs, vb = g.read_planes(0, 1)
+    V = O.dequantize(vw, vs, vb).reshape(n_kv, L, d).astype(np.float64)
+    want = np.repeat(V.mean(axis=1), n_q // n_kv, axis=0)
+    ok, err, nbad = tol_close(out, want, ATOL, RTOL)
+    assert ok, (err, nbad)
+    g.free()
