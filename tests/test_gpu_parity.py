@@ -231,6 +231,82 @@ def test_fused_ignores_stale_nonfinite_tail(E, rng, d, n_q, L):
     assert ok, (err, nbad)
 
 
+def exact_attention(o, q, layer, n_q, n_kv, L):
+    """Attention over the quantized cache in f64: K and V = nibble*scale + bias
+    exactly, softmax(q.K/sqrt(d)) V with the exact max."""
+    nh, d, lmax = o.n_heads, o.head_dim, o.max_seq_len
+    kv = []
+    for k in (0, 1):
+        w, s, b = o.read_planes(layer, k)
+        n = np.concatenate([w & 15, w >> 4], axis=1).astype(np.float64)
+        x = n * s.astype(np.float64)[:, None] + b.astype(np.float64)[:, None]
+        kv.append(x.reshape(nh, lmax, d)[:, :L])
+    K, V = kv
+    qpk = n_q // n_kv
+    out = np.zeros((n_q, d))
+    for h in range(n_q):
+        sc = K[h // qpk] @ q[h].astype(np.float64) / np.sqrt(d)
+        p = np.exp(sc - sc.max())
+        out[h] = p @ V[h // qpk] / p.sum()
+    return out
+
+
+def slope_case(E, rng, d, n_q, n_kv, L, slope, center):
+    """Keys along one direction per kv head, growing with the token index
+    (times `slope`, from -L/2 if `center`), and queries along it: scores that
+    rise (slope > 0) or fall (< 0) by about `slope` per token."""
+    u = rng.standard_normal((n_kv, d))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    t = np.arange(L, dtype=np.float64) - (L / 2 if center else 0)
+    K = (slope * t)[None, :, None] * u[:, None, :] + 0.1 * rng.standard_normal((n_kv, L, d))
+    V = rng.standard_normal((n_kv, L, d))
+    data = np.stack([K, V])[None].astype(np.float32)
+    g, o = pair(E, 1, n_kv, d, L + 8)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    q = (np.repeat(u, n_q // n_kv, axis=0) * np.sqrt(d) +
+         0.3 * rng.standard_normal((n_q, d))).astype(np.float32)
+    sc = o.attention_scores(q, 0, n_q, n_kv)
+    assert abs(float(sc[:, -1].mean() - sc[:, 0].mean())) > 0.5 * abs(slope) * L
+    return g, o, q, float(np.abs(sc).max())
+
+
+@pytest.mark.parametrize("d,n_q,n_kv,L,slope", [
+    (128, 32, 8, 600, 0.2), (128, 64, 8, 600, 0.25), (128, 64, 8, 96, 1.5),
+    (64, 8, 8, 1500, 0.05), (128, 16, 4, 700, -0.2), (64, 32, 4, 90, 1.4)])
+def test_fused_rising_and_falling_scores(E, rng, d, n_q, n_kv, L, slope):
+    """Scores within about +-150: rising ones move the running max again and
+    again (every tile at the steep slopes, in every quad of q heads); falling
+    ones put the max in the first tile and drive the later weights to 0."""
+    say("fused-slope", d, n_q, n_kv, L, slope)
+    g, o, q, smax = slope_case(E, rng, d, n_q, n_kv, L, slope, center=True)
+    assert smax < 160
+    a = g.attention_fused(q, 0, n_q, n_kv)
+    b = o.attention_fused(q, 0, n_q, n_kv)
+    assert np.isfinite(a).all()
+    ok, err, nbad = tol_close(a, b, ATOL, RTOL)
+    assert ok, (err, nbad)
+
+
+@pytest.mark.parametrize("d,n_q,n_kv,L,slope", [(128, 64, 8, 2000, 1.5),
+                                               (128, 32, 8, 3000, 0.25)])
+def test_fused_huge_scores_as_accurate_as_reference(E, rng, d, n_q, n_kv, L, slope):
+    """Scores in the thousands: one f32 ulp of a score (2.4e-4 at 3000) moves
+    its weight by that much relative, so any two f32 orders of the score
+    arithmetic differ by more than the 1e-4 bar (the reference's own order is
+    3e-4 off the exact result here).  Held instead to the exact f64 attention
+    over the same quantized cache: the fused kernel within twice the
+    reference algorithm's error."""
+    say("fused-huge", d, n_q, n_kv, L, slope)
+    g, o, q, smax = slope_case(E, rng, d, n_q, n_kv, L, slope, center=False)
+    assert smax > 700
+    exact = exact_attention(o, q, 0, n_q, n_kv, L)
+    e_gpu = float(np.abs(g.attention_fused(q, 0, n_q, n_kv) - exact).max())
+    e_ref = float(np.abs(o.attention_fused(q, 0, n_q, n_kv) - exact).max())
+    say("  max|score|", smax, "error vs exact: gpu", e_gpu, "reference algorithm", e_ref)
+    assert e_gpu <= 2 * e_ref + 1e-5
+
+
 def test_fused_batch_device(E, rng):
     from eakv_amd.hipmem import DeviceArray
     nl, nh, d, n_q, lmax = 2, 4, 128, 16, 1100
