@@ -62,7 +62,7 @@ void eakv_attention_scores(const eakv_cache_t *cc, const float *queries,
     if (eakvi_enter(c, &prev)) return;
     const size_t qb = (size_t)n_q * c->head_dim * 4;
     const size_t sb = (size_t)n_q * c->seq_len * 4;
-    int rc = eakvi_work_reserve(c, align256(qb) + sb);
+    int rc = eakvi_work_begin(c, c->stream, align256(qb) + sb);
     if (rc == EAKV_OK) {
         float *dq = (float *)c->work;
         float *ds = (float *)((char *)c->work + align256(qb));
@@ -72,6 +72,7 @@ void eakv_attention_scores(const eakv_cache_t *cc, const float *queries,
         if (!e && sb) e = eakvd_memcpy_d2h_async(scores_out, ds, sb, c->stream);
         if (!e) e = eakvd_stream_sync(c->stream);
         if (e) eakvi_hip_fail(e, "attention_scores");
+        eakvi_work_end(c, c->stream);
     }
     eakvi_leave(prev);
 }
@@ -98,11 +99,13 @@ int eakv_attention_output_device(const eakv_cache_t *cc, const float *d_w,
         if (e) rc = eakvi_hip_fail(e, "output");
     }
     if (rc == EAKV_OK)
-        rc = eakvi_work_reserve(c, eakvd_v_sum_work_bytes(&c->geom, c->seq_len, n_q));
+        rc = eakvi_work_begin(c, st, eakvd_v_sum_work_bytes(&c->geom, c->seq_len, n_q));
     if (rc == EAKV_OK) {
         int e = eakvd_v_sum(&c->geom, c->dev, layer, c->seq_len, d_w, n_q, n_kv,
                             d_out, c->work, st);
         if (e) rc = eakvi_hip_fail(e, "v_sum launch");
+        int e2 = eakvi_work_end(c, st);
+        if (rc == EAKV_OK) rc = e2;
     }
     eakvi_leave(prev);
     return rc;
@@ -123,7 +126,7 @@ void eakv_attention_output(const eakv_cache_t *cc, const float *weights,
     const size_t wb = (size_t)n_q * c->seq_len * 4;
     const size_t ob = (size_t)n_q * c->head_dim * 4;
     const size_t pb = eakvd_v_sum_work_bytes(&c->geom, c->seq_len, n_q);
-    int rc = eakvi_work_reserve(c, align256(wb) + align256(ob) + pb);
+    int rc = eakvi_work_begin(c, c->stream, align256(wb) + align256(ob) + pb);
     if (rc == EAKV_OK) {
         float *dw = (float *)c->work;
         float *dout = (float *)((char *)c->work + align256(wb));
@@ -134,6 +137,7 @@ void eakv_attention_output(const eakv_cache_t *cc, const float *weights,
         if (!e) e = eakvd_memcpy_d2h_async(output_out, dout, ob, c->stream);
         if (!e) e = eakvd_stream_sync(c->stream);
         if (e) eakvi_hip_fail(e, "attention_output");
+        eakvi_work_end(c, c->stream);
     }
     eakvi_leave(prev);
 }
@@ -192,10 +196,12 @@ int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
     b.n_seq = n_caches;
     for (int i = 0; i < n_caches; i++) b.seq_len[i] = caches[i]->seq_len;
     if (rc == EAKV_OK)
-        rc = eakvi_work_reserve(c0, eakvd_fused_work_bytes(&c0->geom, &b, n_q));
+        rc = eakvi_work_begin(c0, st, eakvd_fused_work_bytes(&c0->geom, &b, n_q));
     if (rc == EAKV_OK) {
         int e = fused_launch(caches, n_caches, layer, d_q, n_q, n_kv, d_out, st);
         if (e) rc = eakvi_hip_fail(e, "fused launch");
+        int e2 = eakvi_work_end(c0, st);
+        if (rc == EAKV_OK) rc = e2;
     }
     eakvi_leave(prev);
     return rc;
@@ -218,7 +224,7 @@ int eakv_attention_fused(const eakv_cache_t *cc, const float *queries,
     b.seq_len[0] = c->seq_len;
     const size_t io = align256((size_t)n_q * c->head_dim * 4);
     const size_t pb = eakvd_fused_work_bytes(&c->geom, &b, n_q);
-    rc = eakvi_work_reserve(c, 2 * io + pb);
+    rc = eakvi_work_begin(c, c->stream, 2 * io + pb);
     if (rc == EAKV_OK) {
         float *dq = (float *)c->work;
         float *dout = (float *)((char *)c->work + io);
@@ -230,6 +236,7 @@ int eakv_attention_fused(const eakv_cache_t *cc, const float *queries,
                                            c->stream);
         if (!e) e = eakvd_stream_sync(c->stream);
         if (e) rc = eakvi_hip_fail(e, "attention_fused");
+        eakvi_work_end(c, c->stream);
     }
     eakvi_leave(prev);
     return rc;

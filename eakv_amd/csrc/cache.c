@@ -77,10 +77,20 @@ void eakvi_leave(int prev)
     if (eakvd_get_device(&cur) == 0 && cur != prev) eakvd_set_device(prev);
 }
 
-int eakvi_work_reserve(eakv_cache_t *c, size_t n)
+/* Every use of the workspace is ordered after the previous one: uses on the
+ * cache's own stream by that stream; a use on a caller's stream records
+ * work_event there, and the next use (on any stream) waits for it.  Calls
+ * that name the cache with a caller's stream host-wait for the cache's own
+ * stream first (attention.c), which orders the other direction. */
+int eakvi_work_begin(eakv_cache_t *c, void *st, size_t n)
 {
+    if (c->work_on_caller) {
+        int e = eakvd_stream_wait_event(st, c->work_event);
+        if (e) return eakvi_hip_fail(e, "workspace order");
+    }
     if (n <= c->work_bytes) return EAKV_OK;
     int e = eakvd_stream_sync(c->stream);
+    if (!e && c->work_on_caller) e = eakvd_event_sync(c->work_event);
     if (e) return eakvi_hip_fail(e, "stream sync");
     if (c->work) eakvd_free(c->work);
     c->work = NULL;
@@ -92,6 +102,24 @@ int eakvi_work_reserve(eakv_cache_t *c, size_t n)
         return eakvi_hip_fail(e, "workspace hipMalloc");
     }
     c->work_bytes = want;
+    return EAKV_OK;
+}
+
+int eakvi_work_end(eakv_cache_t *c, void *st)
+{
+    if (st == c->stream) {
+        c->work_on_caller = 0;
+        return EAKV_OK;
+    }
+    int e = c->work_event ? 0 : eakvd_event_create(&c->work_event);
+    if (!e) e = eakvd_event_record(c->work_event, st);
+    if (e) {
+        /* the order can no longer be tracked: wait for this use instead */
+        eakvd_stream_sync(st);
+        c->work_on_caller = 0;
+        return eakvi_hip_fail(e, "workspace event");
+    }
+    c->work_on_caller = 1;
     return EAKV_OK;
 }
 
@@ -149,6 +177,8 @@ void eakv_cache_free(eakv_cache_t *c)
     int prev;
     int ok = eakvi_enter(c, &prev) == EAKV_OK;
     if (c->stream) eakvd_stream_sync(c->stream);
+    if (c->work_on_caller) eakvd_event_sync(c->work_event);
+    if (c->work_event) eakvd_event_destroy(c->work_event);
     if (c->work) eakvd_free(c->work);
     if (c->dev) eakvd_free(c->dev);
     if (c->stream) eakvd_stream_destroy(c->stream);
@@ -200,7 +230,8 @@ int eakv_cache_load_raw(eakv_cache_t *c, const float *data, int seq_len)
     int per = (int)((256ll << 20) / (plane_bytes ? plane_bytes : 1));
     if (per < 1) per = 1;
     if (per > n_planes) per = n_planes;
-    rc = eakvi_work_reserve(c, (size_t)plane_bytes * per);
+    rc = eakvi_work_begin(c, c->stream, (size_t)plane_bytes * per);
+    const int began = rc == EAKV_OK;
     for (int p0 = 0; rc == EAKV_OK && p0 < n_planes; p0 += per) {
         int np = n_planes - p0 < per ? n_planes - p0 : per;
         int e = eakvd_memcpy_h2d_async(c->work, data + (int64_t)p0 * row_elems *
@@ -214,6 +245,7 @@ int eakv_cache_load_raw(eakv_cache_t *c, const float *data, int seq_len)
         int e = eakvd_stream_sync(c->stream);
         if (e) rc = eakvi_hip_fail(e, "load_raw");
     }
+    if (began) eakvi_work_end(c, c->stream);
     if (rc == EAKV_OK) c->seq_len = seq_len;
     eakvi_leave(prev);
     return rc;
@@ -261,7 +293,8 @@ int eakv_cache_append(eakv_cache_t *c, const float *data, int layer,
     if (rc) return rc;
     const int64_t row_elems = (int64_t)n_tokens * c->head_dim;
     const size_t bytes = (size_t)row_elems * c->n_kv_heads * 4;
-    rc = eakvi_work_reserve(c, bytes);
+    rc = eakvi_work_begin(c, c->stream, bytes);
+    const int began = rc == EAKV_OK;
     if (rc == EAKV_OK) {
         int e = eakvd_memcpy_h2d_async(c->work, data, bytes, c->stream);
         if (e) rc = eakvi_hip_fail(e, "append H2D");
@@ -273,6 +306,7 @@ int eakv_cache_append(eakv_cache_t *c, const float *data, int layer,
         int e = eakvd_stream_sync(c->stream);
         if (e) rc = eakvi_hip_fail(e, "append");
     }
+    if (began) eakvi_work_end(c, c->stream);
     eakvi_leave(prev);
     return rc;
 }

@@ -50,6 +50,11 @@ int  eakvd_host_free(void *p);
 int  eakvd_stream_create(void **s);
 int  eakvd_stream_destroy(void *s);
 int  eakvd_stream_sync(void *s);
+int  eakvd_event_create(void **e);            /* no timing */
+int  eakvd_event_destroy(void *e);
+int  eakvd_event_record(void *e, void *s);
+int  eakvd_event_sync(void *e);
+int  eakvd_stream_wait_event(void *s, void *e);
 int  eakvd_memset_async(void *p, int v, size_t n, void *s);
 int  eakvd_memcpy_h2d_async(void *dst, const void *src, size_t n, void *s);
 int  eakvd_memcpy_d2h_async(void *dst, const void *src, size_t n, void *s);

@@ -40,6 +40,28 @@ int eakvd_stream_destroy(void *s)
 
 int eakvd_stream_sync(void *s) { return (int)hipStreamSynchronize((hipStream_t)s); }
 
+int eakvd_event_create(void **e)
+{
+    hipEvent_t ev = nullptr;
+    hipError_t r = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    *e = (void *)ev;
+    return (int)r;
+}
+
+int eakvd_event_destroy(void *e) { return e ? (int)hipEventDestroy((hipEvent_t)e) : 0; }
+
+int eakvd_event_record(void *e, void *s)
+{
+    return (int)hipEventRecord((hipEvent_t)e, (hipStream_t)s);
+}
+
+int eakvd_event_sync(void *e) { return (int)hipEventSynchronize((hipEvent_t)e); }
+
+int eakvd_stream_wait_event(void *s, void *e)
+{
+    return (int)hipStreamWaitEvent((hipStream_t)s, (hipEvent_t)e, 0);
+}
+
 int eakvd_memset_async(void *p, int v, size_t n, void *s)
 {
     return (int)hipMemsetAsync(p, v, n, (hipStream_t)s);

@@ -26,6 +26,8 @@ struct eakv_cache {
 
     void  *work;           /* device scratch for staging and partials */
     size_t work_bytes;
+    void  *work_event;     /* recorded after a use of `work` on a caller's stream */
+    int    work_on_caller; /* the last use of `work` was on a caller's stream */
 };
 
 /* error side channel (cache.c) */
@@ -36,9 +38,14 @@ int  eakvi_hip_fail(int hip_err, const char *what);
 int  eakvi_enter(const eakv_cache_t *c, int *prev);
 void eakvi_leave(int prev);
 
-/* Grow the cache's device scratch to at least n bytes (synchronizes the
- * cache's stream before freeing the old buffer). */
-int  eakvi_work_reserve(eakv_cache_t *c, size_t n);
+/* Begin a use of the cache's device scratch on stream st: order st after
+ * the previous use when that was on a caller's stream (a stream wait, no host
+ * wait), and grow the scratch to at least n bytes (waiting for every earlier
+ * use before freeing the old buffer). */
+int  eakvi_work_begin(eakv_cache_t *c, void *st, size_t n);
+/* End a use begun on st (enqueued): on a caller's stream, record the
+ * scratch's event there so that the next use waits for this one. */
+int  eakvi_work_end(eakv_cache_t *c, void *st);
 
 static inline void *eakvi_stream_or_default(const eakv_cache_t *c, void *s)
 {

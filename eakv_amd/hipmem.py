@@ -31,6 +31,8 @@ def hip():
             "hipMemsetAsync": [_vp, C.c_int, C.c_size_t, _vp],
             "hipDeviceSynchronize": [],
             "hipStreamSynchronize": [_vp],
+            "hipStreamCreateWithFlags": [C.POINTER(_vp), C.c_uint],
+            "hipStreamDestroy": [_vp],
             "hipEventCreate": [C.POINTER(_vp)],
             "hipEventDestroy": [_vp],
             "hipEventRecord": [_vp, _vp],
@@ -113,6 +115,24 @@ class DeviceArray:
     def __del__(self):
         try:
             self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    """A non-blocking HIP stream at the default priority."""
+
+    def __init__(self):
+        st = _vp()
+        check(hip().hipStreamCreateWithFlags(C.byref(st), 1), "hipStreamCreateWithFlags")
+        self.s = st.value
+
+    def synchronize(self):
+        check(hip().hipStreamSynchronize(self.s), "hipStreamSynchronize")
+
+    def __del__(self):
+        try:
+            hip().hipStreamDestroy(self.s)
         except Exception:
             pass
 

@@ -13,7 +13,12 @@
  *   - dequantization and the integrity check of GPU-resident planes, which the
  *     reference runs on its host planes from its benchmark and CLI.
  * Device-pointer calls return when the work is enqueued; results are ready
- * after eakv_cache_sync() or a wait on the stream.
+ * after eakv_cache_sync() or a wait on the stream.  Calls on one cache that
+ * use its device workspace (V-sum and fused partials, host staging) are
+ * ordered among themselves whatever their streams (an event recorded on a
+ * caller's stream, waited for by the next use); any other ordering between
+ * streams (e.g. K/V appended on one caller's stream and read on another) is
+ * the caller's, as for any work on two streams.
  */
 #ifndef EAKV_HIP_H
 #define EAKV_HIP_H

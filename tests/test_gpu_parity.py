@@ -328,6 +328,47 @@ def test_fused_batch_device(E, rng):
         assert ok, (lens[i], err, nbad)
 
 
+def test_workspace_ordered_across_caller_streams(E, rng):
+    """Device calls on two caller streams, back to back, share the cache's
+    workspace (the fused chunk partials, the V-sum partials): each call waits
+    for the previous one through an event, so every result matches the
+    oracle; a host call and freeing the cache afterwards wait for them too."""
+    from eakv_amd.hipmem import DeviceArray, Stream
+    nh, d, n_q, L = 8, 128, 32, 8192
+    g, o = loaded(E, rng, nh, d, L, L, 1)
+    sa, sb = Stream(), Stream()
+    qs = [rng.standard_normal((n_q, d)).astype(np.float32) for _ in range(4)]
+    dq = [DeviceArray.from_host(q) for q in qs]
+    dout = [DeviceArray((n_q, d)) for _ in qs]
+    for i in range(len(qs)):
+        st = (sa, sb)[i % 2].s
+        assert E.lib().eakv_attention_fused_batch_device(E.handles([g]), 1, 0, dq[i].ptr,
+                                                         n_q, nh, dout[i].ptr, st) == 0
+    ws = [rng.random((n_q, L)).astype(np.float32) for _ in range(2)]
+    dw = [DeviceArray.from_host(w) for w in ws]
+    dvo = [DeviceArray((n_q, d)) for _ in ws]
+    for i in range(2):
+        assert E.lib().eakv_attention_output_device(g.h, dw[i].ptr, 0, n_q, nh, dvo[i].ptr,
+                                                    (sb, sa)[i].s) == 0
+    # a host call on the cache's own stream right behind them
+    host = g.attention_fused(qs[0], 0, n_q, nh)
+    sa.synchronize()
+    sb.synchronize()
+    for i, q in enumerate(qs):
+        ok, err, nbad = tol_close(dout[i].download(), o.attention_fused(q, 0, n_q, nh),
+                                  ATOL, RTOL)
+        assert ok, (i, err, nbad)
+    assert np.array_equal(host, dout[0].download())
+    for i, w in enumerate(ws):
+        assert np.array_equal(dvo[i].download(), g.attention_output(w, 0, n_q, nh)), i
+    # the last workspace use on a caller's stream, then free
+    assert E.lib().eakv_attention_output_device(g.h, dw[0].ptr, 0, n_q, nh, dvo[1].ptr,
+                                                sa.s) == 0
+    g.free()
+    sa.synchronize()
+    assert np.array_equal(dvo[1].download(), dvo[0].download())
+
+
 def test_device_calls_equal_host_calls(E, rng):
     from eakv_amd.hipmem import DeviceArray
     g, _ = loaded(E, rng, 4, 128, 200, 256)
