@@ -135,6 +135,12 @@ __global__ __launch_bounds__(256) void chunk_sum_kernel(
     out[i] = sum;
 }
 
+__global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ out, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = 0.0f;
+}
+
 }  // namespace
 
 extern "C" size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len,
@@ -151,8 +157,12 @@ extern "C" int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base,
 {
     const hipStream_t st = (hipStream_t)stream;
     const int64_t n_out = (int64_t)n_q * g->head_dim;
-    if (seq_len <= 0)
-        return (int)hipMemsetAsync(out, 0, n_out * sizeof(float), st);
+    if (seq_len <= 0) {
+        // zeros by a kernel, not a memset: the call may be captured in a graph
+        hipLaunchKernelGGL(zero_kernel, dim3((unsigned)ceil_div_i(n_out, 256)), dim3(256), 0,
+                           st, out, n_out);
+        return (int)hipGetLastError();
+    }
     const Planes p = planes_of(*g, base, layer, 1);
     const int n_chunks = ceil_div_i(seq_len, kChunk);
     const int qpk = n_q / n_kv;
