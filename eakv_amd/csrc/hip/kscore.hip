@@ -12,11 +12,82 @@
 // Layout: one lane per token.  A token's 32*gpd packed bytes are read as
 // uint4 vectors; its dequantized values are computed once and dotted with
 // every q head of its group (the reference GQA loop flip).  The q vectors are
-// wave-uniform and are read through the scalar cache.
+// wave-uniform and are read through the scalar cache.  Each block walks
+// several 256-token slices with the next slice's loads in flight while it
+// computes the current one.  Nibbles become floats by masking a dword to four
+// byte-wide nibbles and converting its bytes (v_cvt_f32_ubyte0..3): exact,
+// as the reference's int-to-float conversion of the nibble.
 #include "common.h"
 
 namespace {
 
+// Byte J of x as a float, one v_cvt_f32_ubyteJ (the compiler otherwise
+// extracts the byte with a separate v_bfe_u32 first).
+template <int J>
+__device__ __forceinline__ float ubyte_f32(uint32_t x)
+{
+    float r;
+    if constexpr (J == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+    else if constexpr (J == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+    else if constexpr (J == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+template <int J>
+__device__ __forceinline__ void dequant4(float *klo, float *khi, uint32_t lo, uint32_t hi,
+                                         float s, float b)
+{
+    klo[J] = fmaf(ubyte_f32<J>(lo), s, b);
+    khi[J] = fmaf(ubyte_f32<J>(hi), s, b);
+}
+
+template <int D>
+struct KTok {
+    uint4 raw[2 * (D / 64)];
+    float sc[D / 64], bi[D / 64];
+};
+
+// The packed bytes, scales and biases of the lanes' tokens in slice sl of a
+// kv head whose planes start at w, sc, bi and hold L tokens.  The slice's
+// buffer resources start at the slice (64-bit base arithmetic, wave-uniform)
+// and end at the last token, so the lane offsets are fixed and reads past
+// the last token, or of a slice past the end, return 0.
+template <int D>
+__device__ __forceinline__ void k_load(const uint8_t *w, const float *sc, const float *bi,
+                                       int L, int sl, KTok<D> &T)
+{
+    constexpr int GPD = D / 64;
+    const int64_t t0 = (int64_t)sl * 256;
+    const int64_t left = L > t0 ? L - t0 : 0;            // tokens in this slice and after
+    const int nt = (int)(left < 256 ? left : 256);
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + t0 * GPD * 32),
+                                                      (short)0, nt * GPD * 32, 0x00020000);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(sc + t0 * GPD),
+                                                      (short)0, nt * GPD * 4, 0x00020000);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(bi + t0 * GPD),
+                                                      (short)0, nt * GPD * 4, 0x00020000);
+    const int vw = threadIdx.x * GPD * 32, vs = threadIdx.x * GPD * 4;
+#pragma unroll
+    for (int i = 0; i < 2 * GPD; i++) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, vw + 16 * i, 0, 0);
+        T.raw[i] = uint4{v[0], v[1], v[2], v[3]};
+    }
+    if constexpr (GPD == 2) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b64(rs, vs, 0, 0);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b64(rb, vs, 0, 0);
+        T.sc[0] = __uint_as_float(a[0]);
+        T.sc[1] = __uint_as_float(a[1]);
+        T.bi[0] = __uint_as_float(b[0]);
+        T.bi[1] = __uint_as_float(b[1]);
+    } else {
+        T.sc[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, vs, 0, 0));
+        T.bi[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, vs, 0, 0));
+    }
+}
+
+// Block b takes the 256-token slices b, b + gridDim.x, ... of its kv head
+// (one token per lane) and loads the next slice while it computes one.
 template <int D>
 __global__ __launch_bounds__(256) void k_score_kernel(
     const uint8_t *__restrict__ kw, const float *__restrict__ ks,
@@ -26,47 +97,86 @@ __global__ __launch_bounds__(256) void k_score_kernel(
     constexpr int GPD = D / 64;
     constexpr int NC = D / 16;
     const int kvh = blockIdx.y;
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (t >= L) return;
+    const int n_sl = (L + 255) / 256;
+    const int64_t hb = (int64_t)kvh * gph;        // the kv head's first group
+    const uint8_t *hw = kw + hb * 32;
+    const float *hs = ks + hb, *hbi = kb + hb;
+    const float *qk = q + (int64_t)kvh * qpk * D;
 
-    const int64_t g0 = (int64_t)kvh * gph + (int64_t)t * GPD;
-    const uint4 *src = reinterpret_cast<const uint4 *>(kw + g0 * 32);
-    uint4 raw[2 * GPD];
+    // one 256-token slice: dequantize each lane's token once, then dot it
+    // with every q head of the kv head
+    auto compute = [&](const KTok<D> &T, int sl) {
+        const int t = sl * 256 + threadIdx.x;
+        // k[c*16 + i]: chunk c = 4*grp + 2*nib + half, byte i of half `half`
+        float k[D];
 #pragma unroll
-    for (int i = 0; i < 2 * GPD; i++) raw[i] = src[i];
-    float sc[GPD], bi[GPD];
+        for (int grp = 0; grp < GPD; grp++)
 #pragma unroll
-    for (int j = 0; j < GPD; j++) {
-        sc[j] = ks[g0 + j];
-        bi[j] = kb[g0 + j];
-    }
-
-    float k[D];
+            for (int half = 0; half < 2; half++) {
+                const uint4 v = T.raw[grp * 2 + half];
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
-        const int grp = c >> 2, cc = c & 3;
-        const uint4 &v = raw[grp * 2 + (cc & 1)];
+                for (int wd = 0; wd < 4; wd++) {
+                    const uint32_t lo = w4[wd] & 0x0f0f0f0fu;
+                    const uint32_t hi = (w4[wd] >> 4) & 0x0f0f0f0fu;
+                    float *klo = &k[(4 * grp + half) * 16 + 4 * wd];
+                    float *khi = &k[(4 * grp + 2 + half) * 16 + 4 * wd];
+                    dequant4<0>(klo, khi, lo, hi, T.sc[grp], T.bi[grp]);
+                    dequant4<1>(klo, khi, lo, hi, T.sc[grp], T.bi[grp]);
+                    dequant4<2>(klo, khi, lo, hi, T.sc[grp], T.bi[grp]);
+                    dequant4<3>(klo, khi, lo, hi, T.sc[grp], T.bi[grp]);
+                }
+            }
+        for (int o = 0; o < qpk; o++) {
+            const float *qv = qk + (int64_t)o * D;
+            float acc[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            uint32_t b = byte_of(v, i);
-            uint32_t n = cc < 2 ? (b & 15u) : (b >> 4);
-            k[c * 16 + i] = fmaf((float)n, sc[grp], bi[grp]);
+            for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    acc[i] = fmaf(k[c * 16 + i], qv[c * 16 + i], acc[i]);
+            if (t < L)
+                scores[(int64_t)(kvh * qpk + o) * L + t] = __fmul_rn(reduce16(acc), rs);
         }
-    }
+    };
 
-    for (int o = 0; o < qpk; o++) {
-        const int qh = kvh * qpk + o;
-        const float *qv = q + (int64_t)qh * D;
-        float acc[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NC; c++)
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                acc[i] = fmaf(k[c * 16 + i], qv[c * 16 + i], acc[i]);
-        scores[(int64_t)qh * L + t] = __fmul_rn(reduce16(acc), rs);
+    // two buffers in turn: the next slice loads into one while the other is
+    // consumed (no copies between them, so the consumer waits only for its
+    // own loads)
+    const int G = gridDim.x;
+    KTok<D> b0, b1;
+    int sl = blockIdx.x;
+    // the loads of the next slice are unconditional (past the end they read
+    // 0 and cost no memory traffic), so every path waits for the same loads
+    k_load<D>(hw, hs, hbi, L, sl, b0);
+    for (;;) {
+        k_load<D>(hw, hs, hbi, L, sl + G, b1);
+        compute(b0, sl);
+        sl += G;
+        if (sl >= n_sl) break;
+        k_load<D>(hw, hs, hbi, L, sl + G, b0);
+        compute(b1, sl);
+        sl += G;
+        if (sl >= n_sl) break;
     }
+}
+
+// Blocks per kv head: two waves per SIMD over the chip, at most one per
+// 256-token slice.
+int k_blocks(int n_sl, int n_kv)
+{
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, v = 0;
+        n_cu = hipGetDevice(&dev) == hipSuccess &&
+                       hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                           hipSuccess && v > 0
+                   ? v : 256;
+    }
+    const int want = (2 * n_cu + n_kv - 1) / n_kv;
+    return want < n_sl ? want : n_sl;
 }
 
 }  // namespace
@@ -78,7 +188,7 @@ extern "C" int eakvd_k_score(const eakvd_geom *g, const uint8_t *base,
     if (seq_len <= 0) return 0;
     const Planes p = planes_of(*g, base, layer, 0);
     const hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((unsigned)ceil_div_i(seq_len, 256), (unsigned)n_kv);
+    const dim3 grid((unsigned)k_blocks(ceil_div_i(seq_len, 256), n_kv), (unsigned)n_kv);
     const int qpk = n_q / n_kv;
     const float rs = 1.0f / sqrtf((float)g->head_dim);
     if (g->head_dim == 64)

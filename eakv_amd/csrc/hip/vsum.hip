@@ -17,7 +17,7 @@
 // slot at a time and issues all their loads (V word, scale, bias, weights)
 // before the arithmetic, so kBatch loads per lane are in flight; a block
 // covers a chunk of kChunk tokens of one kv head and writes one partial per
-// q head, which chunk_sum_kernel adds in chunk order.
+// q head, which chunk_sum_kernel adds in a fixed order.
 #include "common.h"
 
 namespace {
@@ -114,25 +114,42 @@ __global__ __launch_bounds__(256) void v_sum_kernel(
     }
 }
 
-// out[i] = sum over chunks in order of partial[c][i], the chunks read 8 at
-// a time with their loads in flight
+// out[i] = the sum over chunks of partial[c][i], in a fixed order: a block
+// takes 32 outputs; thread (i, part) adds chunks part, part + 8, ... in
+// order, kSumBatch at a time with their loads in flight (32 consecutive
+// outputs per row of threads: coalesced), and the 8 part sums of an output
+// are then added in part order.
+constexpr int kSumParts = 8;
+constexpr int kSumBatch = 16;
+
 __global__ __launch_bounds__(256) void chunk_sum_kernel(
     const float *__restrict__ partial, int n_chunks, int64_t n_out,
     float *__restrict__ out)
 {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n_out) return;
-    float sum = partial[i];
-    for (int c0 = 1; c0 < n_chunks; c0 += 8) {
-        float p[8];
+    __shared__ float red[kSumParts][32];
+    const int o = threadIdx.x & 31, part = threadIdx.x >> 5;
+    const int64_t i = (int64_t)blockIdx.x * 32 + o;
+    const int64_t ic = i < n_out ? i : n_out - 1;
+    float sum = 0.0f;
+    for (int c0 = part; c0 < n_chunks; c0 += kSumParts * kSumBatch) {
+        float p[kSumBatch];
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            p[j] = c0 + j < n_chunks ? partial[(int64_t)(c0 + j) * n_out + i] : 0.0f;
+        for (int j = 0; j < kSumBatch; j++) {
+            const int c = c0 + j * kSumParts;
+            p[j] = c < n_chunks ? partial[(int64_t)c * n_out + ic] : 0.0f;
+        }
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (c0 + j < n_chunks) sum = __fadd_rn(sum, p[j]);
+        for (int j = 0; j < kSumBatch; j++)
+            if (c0 + j * kSumParts < n_chunks) sum = __fadd_rn(sum, p[j]);
     }
-    out[i] = sum;
+    red[part][o] = sum;
+    __syncthreads();
+    if (part == 0 && i < n_out) {
+        float t = red[0][o];
+#pragma unroll
+        for (int k = 1; k < kSumParts; k++) t = __fadd_rn(t, red[k][o]);
+        out[i] = t;
+    }
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ out, int64_t n)
@@ -175,7 +192,7 @@ extern "C" int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base,
                        : qpk <= 4 ? v_sum_kernel<128, 4> : v_sum_kernel<128, 8>);
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, p.w, p.s, p.b, g->gph, seq_len, w, n_q,
                        qpk, partial);
-    hipLaunchKernelGGL(chunk_sum_kernel, dim3((unsigned)ceil_div_i(n_out, 256)),
+    hipLaunchKernelGGL(chunk_sum_kernel, dim3((unsigned)ceil_div_i(n_out, 32)),
                        dim3(256), 0, st, partial, n_chunks, n_out, out);
     return (int)hipGetLastError();
 }
