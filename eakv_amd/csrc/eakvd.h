@@ -96,6 +96,13 @@ size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len, int n_q);
 int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base, int layer,
                 int seq_len, const float *w, int n_q, int n_kv, float *out,
                 void *work, void *stream);
+/* The same on the matrix cores (hip/fused.hip), for 2 to 8 q heads per kv
+ * head; returns -1 without launching anything where it does not apply.
+ * eakvd_v_sum tries it first. */
+size_t eakvd_v_sum_mfma_work_bytes(const eakvd_geom *g, int seq_len, int n_q);
+int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int layer,
+                     int seq_len, const float *w, int n_q, int n_kv, float *out,
+                     void *work, void *stream);
 
 /* Fused decode attention over a batch of same-geometry caches:
  * out[s][qh][i] = softmax_t(q[s][qh].K[s][kv][t] / sqrt(d)) . V[s][kv][t][i]

@@ -33,6 +33,8 @@
 //   Waves are merged in LDS, chunks by merge_kernel.
 // valu_kernel (wider groups): one lane per token for K with the reference
 //   arithmetic, then V by dims; same partial/merge scheme.
+#include <string.h>
+
 #include <type_traits>
 
 #include "common.h"
@@ -110,6 +112,13 @@ struct Stage {
     uint2 kw[Geo<D>::NK][Geo<D>::GPD];
 };
 
+// V-sum mode: one lane's weights of a pipeline stage (score layout: head
+// 4hq + l/16 of quad hq, token 16k + l%16 of sub-tile k).
+template <int D, int HH>
+struct WStage {
+    float wv[HH][Geo<D>::NK];
+};
+
 // The scales and biases of one tile for this lane's tokens (score layout:
 // token 16k + tl), read from the LDS slot.
 template <int D>
@@ -155,6 +164,24 @@ __device__ __forceinline__ void load_k(Stage<D> &T, const LaneOffs &P, int dt)
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
             T.kw[k][gg] = ldb64(P.kw, P.kwo, ws + (16 * k * GPD + gg) * 32);
+}
+
+// V-sum mode: the weights of the tile at token offset dt, w[head][dt + 16k +
+// tl] from the kv head's rows (wo[hq]: byte offset of the lane's row).
+// Tokens past the sequence read the row's last weight (in bounds); the
+// caller masks them.
+template <int D, int HH>
+__device__ __forceinline__ void load_w(WStage<D, HH> &T, __amdgpu_buffer_rsrc_t r,
+                                       const uint32_t *wo, int dt, int tl, int L)
+{
+#pragma unroll
+    for (int hq = 0; hq < HH; hq++)
+#pragma unroll
+        for (int k = 0; k < Geo<D>::NK; k++) {
+            const int t = min(dt + 16 * k + tl, L - 1);
+            T.wv[hq][k] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(r, (int)(wo[hq] + 4u * (uint32_t)t), 0, 0));
+        }
 }
 
 // The V bytes of the tile at dt into a V slot, 1 KB per instruction (buffer
@@ -367,13 +394,23 @@ struct WaveState {
 // four heads: each quad has its own q digits (K MFMA rows), softmax state,
 // digit rows and V MFMAs; the K bytes, the V tile in LDS and the nibbles
 // taken from them are shared, so the planes are read once for all G heads.
-template <int D, int HH>
+//
+// VS: the V-sum of the unfused API, o = sum_t w[h][t] v[t] with the weights
+// given (q points to w[n_q][L] of one sequence).  No K, no softmax: each
+// tile's weights are loaded in place of its K bytes and go straight to the
+// digit rows (signed fixed point, the exponent from the largest |a|); m
+// stays 0, the merge adds the chunks unnormalised, and a non-finite weight
+// makes its head's output NaN (lsum carries the flag).
+template <int D, int HH, bool VS>
 __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, HH> / 4)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
     int n_q, int qpk, float rs, float *__restrict__ part)
 {
     constexpr int GPD = D / 64;
     constexpr int NK = Geo<D>::NK;
+    // VGPR loads per group after the V and scale loads: K bytes, or weights
+    constexpr int NKL = VS ? NK * HH : kNK<D>;
+    using StageT = std::conditional_t<VS, WStage<D, HH>, Stage<D>>;
     constexpr int NW = kWavesH<HH>;                     // waves per block
     // Per wave: kSlots V and scale slots and the digit rows of its HH
     // quads; after the tiles the wave's V slots 0 (and 1) hold its outputs
@@ -425,6 +462,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
     bool qrow[HH];
     float qv[HH][GPD][16];
+    if constexpr (!VS)
 #pragma unroll
     for (int hq = 0; hq < HH; hq++) {
         qrow[hq] = 4 * hq + ha < G;
@@ -449,6 +487,10 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     for (int hq = 0; hq < HH; hq++) live[hq] = 4 * hq + ho < G;
 
     LaneOffs P;
+    // V-sum: the weight rows of the kv head (unused otherwise)
+    const __amdgpu_buffer_rsrc_t wr = plane_rsrc(
+        q + (VS ? (int64_t)kvh * qpk * L : 0), VS ? (int64_t)qpk * L * 4 : 0);
+    uint32_t wo[HH];
     {
         const int64_t wbytes = g.max_groups * 32;
         P.kw = plane_rsrc(K.w, wbytes);
@@ -457,7 +499,8 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         // scale and bias planes of both
         P.layer = plane_rsrc(K.w, 2 * g.block_bytes);
         // scale load: lane l fetches bytes 16e.. of plane pl's tile
-        const int pl = GPD == 2 ? l >> 4 : (l & 31) >> 3;
+        // (V-sum: only the V planes; lanes of the K planes fetch them again)
+        const int pl = (GPD == 2 ? l >> 4 : (l & 31) >> 3) | (VS ? 2 : 0);
         const int e = GPD == 2 ? l & 15 : l & 7;
         const int64_t poff = (pl & 2 ? g.block_bytes : 0) + (pl & 1 ? g.b_off : g.s_off);
         P.sco = (uint32_t)(poff + hbase * 4 + 16 * e);
@@ -467,6 +510,12 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         const int vt = l / Geo<D>::UPT;
         const int vu = (l % Geo<D>::UPT) ^ vswz<D>(vt);
         P.vwo = (uint32_t)(hbase * 32 + vt * Geo<D>::RB + 16 * vu);
+        if constexpr (VS) {
+            // lane (ho, tl): row kvh*qpk + 4hq + ho (head 0 past the group), token tl
+#pragma unroll
+            for (int hq = 0; hq < HH; hq++)
+                wo[hq] = (uint32_t)((live[hq] ? 4 * hq + ho : 0) * L * 4);
+        }
     }
 
     // LDS read/write offsets of this lane (wave-relative, bytes).
@@ -537,7 +586,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // unit's last tile (in bounds; their scores are masked)
     auto ldt = [&](int t) { return min(t, n_tiles - 1) * kTT; };
 
-    Stage<D> st[kSlots];
+    StageT st[kSlots];
     // group j: V of tile T(j-1) into V slot (j-1) % kSlots, then the scales
     // and K bytes of tile T(j) into scale slot and stage j % kSlots
     auto load_group = [&](auto jc, int tv, int tkk) {
@@ -546,7 +595,8 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         __builtin_amdgcn_sched_barrier(0);
         load_scales<D>(sslot(std::integral_constant<int, j % kSlots>{}), P, ldt(tkk));
         __builtin_amdgcn_sched_barrier(0);
-        load_k<D>(st[j % kSlots], P, ldt(tkk));
+        if constexpr (VS) load_w<D, HH>(st[j % kSlots], wr, wo, ldt(tkk), tl, L);
+        else load_k<D>(st[j % kSlots], P, ldt(tkk));
         __builtin_amdgcn_sched_barrier(0);
     };
     // Unconditional (a wave without tiles reads the unit's last tile), so
@@ -562,7 +612,8 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     __builtin_amdgcn_sched_barrier(0);
     load_scales<D>(sslot(I0{}), P, ldt(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
-    load_k<D>(st[0], P, ldt(tk[0]));
+    if constexpr (VS) load_w<D, HH>(st[0], wr, wo, ldt(tk[0]), tl, L);
+    else load_k<D>(st[0], P, ldt(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
     fetch(ring[1]);
     load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
@@ -579,6 +630,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     const float rs2 = rs * EAKV_LOG2E;
     v4i A[HH][GPD];
     float kwl[HH], kwh[HH], bq[HH][GPD];
+    if constexpr (!VS)
 #pragma unroll
     for (int hq = 0; hq < HH; hq++) {
     float amax = 0.0f;
@@ -638,7 +690,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             S[hq].wh[gg] = S[hq].wl[gg] = 0.0f;
         }
         S[hq].lsum = 0.0f;
-        S[hq].m = -INFINITY;
+        S[hq].m = VS ? 0.0f : -INFINITY;
     }
 
     // The weights of one tile from its scores and the running max m:
@@ -656,7 +708,9 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         psum = 0.0f;
 #pragma unroll
         for (int k = 0; k < NK; k++) {
-            p[k] = live[hq] ? __builtin_amdgcn_exp2f(sc[k] - m) : 0.0f;
+            // V-sum: sc holds the tile's (masked) weights
+            if constexpr (VS) p[k] = sc[k];
+            else p[k] = live[hq] ? __builtin_amdgcn_exp2f(sc[k] - m) : 0.0f;
             psum += p[k];
         }
 #pragma unroll
@@ -667,7 +721,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             for (int k = 0; k < NK; k++) {
                 a[k] = mul_zero(p[k], C.vs[k][gg]);
                 bi[gg] += mul_zero(p[k], C.vb[k][gg]);
-                am = max_pos(am, a[k]);
+                am = max_pos(am, VS ? fabsf(a[k]) : a[k]);
             }
             am = row_max16_pos(am);
             const int E = 30 - __builtin_amdgcn_frexp_expf(am);
@@ -747,6 +801,36 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         softmax(C, sc);
     };
 
+    // V-sum: the weights of the tile at dt (past the sequence and for heads
+    // past the group: 0) to the digit rows, sum w*bias per (head, group) to
+    // bacc; a non-finite weight sets the head's lsum to NaN.
+    auto vs_weights = [&](const auto &T, const Scales<D> &C, int dt) {
+        float pw[HH][NK];
+        bool bad[HH];
+#pragma unroll
+        for (int hq = 0; hq < HH; hq++) {
+            bad[hq] = false;
+#pragma unroll
+            for (int k = 0; k < NK; k++) {
+                const bool in = live[hq] && dt + 16 * k + tl < L;
+                pw[hq][k] = in ? T.wv[hq][k] : 0.0f;
+                bad[hq] = bad[hq] || !(fabsf(pw[hq][k]) <= 3.40282347e38f);
+            }
+        }
+        float psum, bi[GPD];
+        weights(std::integral_constant<int, 0>{}, C, pw[0], 0.0f, psum, bi);
+#pragma unroll
+        for (int gg = 0; gg < GPD; gg++) S[0].bacc[gg] += bi[gg];
+        if constexpr (HH > 1) {
+            weights(std::integral_constant<int, 1>{}, C, pw[1], 0.0f, psum, bi);
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) S[1].bacc[gg] += bi[gg];
+        }
+#pragma unroll
+        for (int hq = 0; hq < HH; hq++)
+            if (bad[hq]) S[hq].lsum = __builtin_nanf("");
+    };
+
     // V(tile in vslot) with the digits in the digit rows: the transposed
     // reads (vread), then the 4*GPD MFMA pairs, then their recombination, so
     // the MFMA latency is covered by the MFMAs behind it (vsum).
@@ -807,22 +891,24 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // V(T(i)) and K(T(i+1)) with its softmax (digits of T(i+1)).  kSlots-1
     // groups stay in flight behind the one consumed (rotating registers and
     // LDS slots).
-    constexpr int kLater = (kSlots - 1) * kGroup<D>;    // loads of the groups after the oldest
-    constexpr int kEarly = (kSlots - 2) * kGroup<D>;
+    constexpr int kGrp = Geo<D>::NVD + kDma<D> + NKL;   // loads per group
+    constexpr int kLater = (kSlots - 1) * kGrp;         // loads of the groups after the oldest
+    constexpr int kEarly = (kSlots - 2) * kGrp;
     if (tk[0] < n_tiles) {
         {
             Scales<D> C;
             // group 0 (scales, K of T(0)) is complete once at most its K
             // loads and all later groups are outstanding
-            wait_vm<kNK<D> + kLater>();
+            wait_vm<NKL + kLater>();
             read_scales<D>(sslot(I0{}), tl, C);
-            kscores_softmax(st[0], C, tk[0] * kTT);
+            if constexpr (VS) vs_weights(st[0], C, tk[0] * kTT);
+            else kscores_softmax(st[0], C, tk[0] * kTT);
         }
         // iteration i = r (mod kSlots)
         auto iter = [&](auto rc) {
             constexpr int r = decltype(rc)::value;
             // V(T(i)): its loads were the first of group i+1
-            wait_vm<kDma<D> + kNK<D> + kEarly>();
+            wait_vm<kDma<D> + NKL + kEarly>();
             VRead R;
             vread(vslot(rc), R);
             if constexpr (HH == 1) {
@@ -837,9 +923,10 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             vsum(R);
             // K(T(i+1)): scales, then bytes (the compiler waits for those)
             Scales<D> C;
-            wait_vm<kNK<D> + kLater>();
+            wait_vm<NKL + kLater>();
             read_scales<D>(sslot(std::integral_constant<int, (r + 1) % kSlots>{}), tl, C);
-            kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * kTT);
+            if constexpr (VS) vs_weights(st[(r + 1) % kSlots], C, tk[1] * kTT);
+            else kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * kTT);
             const bool more = tk[1] < n_tiles;
 #pragma unroll
             for (int j = 0; j < kSlots; j++) tk[j] = __builtin_amdgcn_readfirstlane(tk[j + 1]);
@@ -912,13 +999,14 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
 
 // Merge of the MFMA program's chunk partials (log2 domain) per (q head,
 // sequence): M = max(-1e6 log2(e), m_c) (the reference's max starts at
-// -1e6), l = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M), out = o * (1/l).
+// -1e6), l = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M), out = o * (1/l)
+// (V-sum: out = o).
 // The chunks are read kMergeBatch at a time with all loads in flight and
 // merged online across batches.  An empty sequence has no chunks:
 // 0 * (1/0) = NaN, as the reference.
 constexpr int kMergeBatch = 16;
 
-template <int D>
+template <int D, bool VS>
 __global__ __launch_bounds__(D) void merge_kernel(
     eakvd_batch bt, int n_q, int max_chunks, int wpb, const float *__restrict__ part,
     float *__restrict__ out)
@@ -953,7 +1041,10 @@ __global__ __launch_bounds__(D) void merge_kernel(
         }
         M = Mn;
     }
-    out[((int64_t)s * n_q + qh) * D + i] = ot * (1.0f / lt);
+    // V-sum: the plain sum (m = 0 in every chunk); lt is 0, or NaN after a
+    // non-finite weight
+    if constexpr (VS) out[((int64_t)s * n_q + qh) * D + i] = lt == lt ? ot : lt;
+    else out[((int64_t)s * n_q + qh) * D + i] = ot * (1.0f / lt);
 }
 
 // ------------------------------------------------------------------ VALU
@@ -1193,16 +1284,17 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv, per_cu);
         const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
         const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
-        auto kern = g->head_dim == 64 ? (hh == 1 ? mfma_kernel<64, 1> : mfma_kernel<64, 2>)
-                                      : (hh == 1 ? mfma_kernel<128, 1> : mfma_kernel<128, 2>);
+        auto kern = g->head_dim == 64
+                        ? (hh == 1 ? mfma_kernel<64, 1, false> : mfma_kernel<64, 2, false>)
+                        : (hh == 1 ? mfma_kernel<128, 1, false> : mfma_kernel<128, 2, false>);
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, qpk, rs,
                            part);
         if (g->head_dim == 64)
-            hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc, wpb,
-                               part, out);
+            hipLaunchKernelGGL((merge_kernel<64, false>), mgrid, dim3(64), 0, st, *b, n_q, mc,
+                               wpb, part, out);
         else
-            hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc, wpb,
-                               part, out);
+            hipLaunchKernelGGL((merge_kernel<128, false>), mgrid, dim3(128), 0, st, *b, n_q, mc,
+                               wpb, part, out);
         return (int)hipGetLastError();
     }
     const int mc = (ml + kChunkV - 1) / kChunkV;
@@ -1222,5 +1314,54 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
     else
         hipLaunchKernelGGL(combine_kernel<128>, cgrid, dim3(128), 0, st, *b, n_q,
                            mc, part, out);
+    return (int)hipGetLastError();
+}
+
+// The unfused V-sum on the matrix cores (mfma_kernel in V-sum mode) for 2 to
+// 8 q heads per kv head: out[n_q][D] = sum_t w[h][t] V[t] over seq_len
+// tokens of one cache, the chunk partials in `work`.  Returns -1 (nothing
+// launched) where it does not apply: MHA (one q head per kv head fills a
+// quarter of each MFMA; the VALU kernel measured as fast or faster there),
+// more than 8 q heads per kv head, planes beyond 32-bit buffer offsets, or
+// weights beyond 2 GiB.
+extern "C" size_t eakvd_v_sum_mfma_work_bytes(const eakvd_geom *g, int seq_len, int n_q)
+{
+    const int mc = (seq_len + kChunkV - 1) / kChunkV;
+    return (size_t)n_q * (mc > 0 ? mc : 1) * (g->head_dim + 2) * sizeof(float);
+}
+
+extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int layer,
+                                int seq_len, const float *w, int n_q, int n_kv, float *out,
+                                void *work, void *stream)
+{
+    const int qpk = n_q / n_kv;
+    if (qpk < 2 || qpk > 8 || 2 * g->block_bytes > (int64_t)0x7fffffff ||
+        (int64_t)qpk * seq_len * 4 > (int64_t)0x7fffffff || seq_len <= 0)
+        return -1;
+    const hipStream_t st = (hipStream_t)stream;
+    eakvd_batch b;
+    memset(&b, 0, sizeof(b));
+    b.n_seq = 1;
+    b.base[0] = base;
+    b.seq_len[0] = seq_len;
+    const int hh = qpk <= 4 ? 1 : 2;
+    const int per_cu = g->head_dim == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
+                                         : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
+    const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
+    const int mc = mfma_blocks_per_unit(seq_len, n_kv, per_cu);
+    const dim3 grid((unsigned)mc, (unsigned)n_kv, 1u);
+    const dim3 mgrid((unsigned)n_q, 1u);
+    float *part = (float *)work;
+    auto kern = g->head_dim == 64
+                    ? (hh == 1 ? mfma_kernel<64, 1, true> : mfma_kernel<64, 2, true>)
+                    : (hh == 1 ? mfma_kernel<128, 1, true> : mfma_kernel<128, 2, true>);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, b, layer, w, n_q, qpk, 0.0f,
+                       part);
+    if (g->head_dim == 64)
+        hipLaunchKernelGGL((merge_kernel<64, true>), mgrid, dim3(64), 0, st, b, n_q, mc, wpb,
+                           part, out);
+    else
+        hipLaunchKernelGGL((merge_kernel<128, true>), mgrid, dim3(128), 0, st, b, n_q, mc, wpb,
+                           part, out);
     return (int)hipGetLastError();
 }

@@ -165,7 +165,9 @@ extern "C" size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len,
 {
     if (seq_len <= 0) return 0;
     const int n_chunks = ceil_div_i(seq_len, kChunk);
-    return (size_t)n_chunks * n_q * g->head_dim * sizeof(float);
+    const size_t valu = (size_t)n_chunks * n_q * g->head_dim * sizeof(float);
+    const size_t mfma = eakvd_v_sum_mfma_work_bytes(g, seq_len, n_q);
+    return valu > mfma ? valu : mfma;
 }
 
 extern "C" int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base,
@@ -180,6 +182,9 @@ extern "C" int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base,
                            st, out, n_out);
         return (int)hipGetLastError();
     }
+    // the matrix-core program where it applies (up to 8 q heads per kv head)
+    const int r = eakvd_v_sum_mfma(g, base, layer, seq_len, w, n_q, n_kv, out, work, stream);
+    if (r >= 0) return r;
     const Planes p = planes_of(*g, base, layer, 1);
     const int n_chunks = ceil_div_i(seq_len, kChunk);
     const int qpk = n_q / n_kv;

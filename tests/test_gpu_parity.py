@@ -195,6 +195,35 @@ def test_v_sum_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
         assert np.all(err <= 1e-4 + 4e-7 * mag), (err.max(), (err / mag).max())
 
 
+@pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", [
+    (8, 32, 8, 128, 3000, 3000), (4, 32, 4, 64, 1000, 1024), (2, 2, 2, 128, 77, 80),
+    (2, 12, 2, 128, 513, 520)])
+def test_v_sum_signed_and_nonfinite_weights(E, rng, nh, n_q, n_kv, d, L, lmax):
+    """Weights of either sign (the V-sum takes any weights, not only softmax
+    rows): within 1e-4 + 4e-7 * sum|w*v| of the exact f64 sum, as the
+    reference's single fma chain.  A NaN weight in a head's row makes that
+    head's output NaN, as in the reference's chain; the other heads are
+    unaffected."""
+    say("vsum-signed", nh, n_q, n_kv, d, L)
+    g, o = loaded(E, rng, nh, d, L, lmax)
+    w = (rng.standard_normal((n_q, L)) * np.exp(rng.uniform(-3, 3, (n_q, 1)))).astype(np.float32)
+    vw, vs, vb = o.read_planes(1, 1)
+    Vd = O.dequantize(vw, vs, vb).reshape(nh, lmax, d)[:n_kv, :L].astype(np.float64)
+    Vd = np.repeat(Vd, n_q // n_kv, axis=0)
+    exact = np.einsum("ht,htd->hd", w.astype(np.float64), Vd)
+    mag = np.einsum("ht,htd->hd", np.abs(w.astype(np.float64)), np.abs(Vd))
+    for got in (g.attention_output(w, 1, n_q, n_kv), o.attention_output(w, 1, n_q, n_kv)):
+        err = np.abs(got - exact)
+        assert np.all(err <= 1e-4 + 4e-7 * mag), (err.max(), (err / mag).max())
+    w[1, L // 2] = np.nan
+    got = g.attention_output(w, 1, n_q, n_kv)
+    assert np.isnan(got[1]).all()
+    assert np.isnan(o.attention_output(w, 1, n_q, n_kv)[1]).all()
+    keep = [h for h in range(n_q) if h != 1]
+    err = np.abs(got[keep] - exact[keep])
+    assert np.all(err <= 1e-4 + 4e-7 * mag[keep]), err.max()
+
+
 @pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", SHAPES)
 def test_fused_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
     say("fused", nh, n_q, n_kv, d, L)
