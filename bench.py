@@ -199,8 +199,13 @@ class Workload:
 
 
 def cpu_baseline(cfg, budget_s=12.0):
-    """Time the oracle's two-pass fused attention (one sequence, one layer,
-    all q heads, full context) single-threaded and on up to 16 threads."""
+    """Time the reference's CPU fused attention (the oracle's two-pass
+    restatement of fused_attention.ea, on AVX-512 where the host has it, as
+    the reference's kernels compile; else the scalar restatement) over one
+    sequence x one layer, all q heads, full context: the median of up to 50
+    single-threaded runs after a warmup, then up to 24 units per thread spread
+    over up to 16 threads (10-20 s of CPU work at the 32K configuration).
+    Per layer = per unit x the configuration's sequences."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     nkv, nq, d, L = cfg["nkv"], cfg["nq"], cfg["d"], cfg["L"]
@@ -209,26 +214,36 @@ def cpu_baseline(cfg, budget_s=12.0):
     data = rng.standard_normal((1, 2, nkv, L, d), dtype=np.float32)
     oc.load_raw(data, L)
     del data
-    q = rng.standard_normal((nq, d), dtype=np.float32)
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    avx = O.avx512_available()
+    run = (lambda: oc.attention_fused_avx512(q, 0, nq, nkv)) if avx else \
+        (lambda: oc.attention_fused(q, 0, nq, nkv))
     t0 = time.perf_counter()
-    oc.attention_fused(q, 0, nq, nkv)
-    single = time.perf_counter() - t0
+    run()                                                   # warmup
+    first = time.perf_counter() - t0
+    n1 = int(max(3, min(50, budget_s / 2 / max(first, 1e-4))))
+    times = []
+    for _ in range(n1):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    single = float(np.median(times))
     threads = max(1, min(16, os.cpu_count() or 1))
-    # one unit per thread, more while the budget allows
-    reps = threads * max(1, int(budget_s / max(single, 1e-3) / 2))
-    reps = min(reps, 4 * threads)
+    reps = threads * max(1, min(24, int(budget_s / 2 / max(single, 1e-4) / 2)))
     t0 = time.perf_counter()
     with ThreadPoolExecutor(threads) as ex:
-        list(ex.map(lambda _: oc.attention_fused(q, 0, nq, nkv), range(reps)))
-    allcore = (time.perf_counter() - t0) / reps            # s per (seq, layer) unit
+        list(ex.map(lambda _: run(), range(reps)))
+    allcore = (time.perf_counter() - t0) / reps             # s per unit, all threads busy
     per_layer_us = lambda unit_s: unit_s * cfg["nseq"] * 1e6
+    what = ("AVX-512 restatement (16-lane intrinsics, bit-identical to the scalar oracle)"
+            if avx else "scalar C restatement (this host lacks AVX-512)")
     return {
         "value": round(per_layer_us(allcore), 1), "unit": "us/layer",
-        "cores": threads, "kind": "port",
+        "cores": threads, "kind": "port", "isa": "avx512" if avx else "scalar",
         "single_core_us_per_layer": round(per_layer_us(single), 1),
-        "sample": (f"oracle two-pass fused attention (C restatement of "
-                   f"fused_attention.ea, extended to GQA), 1 sequence x 1 layer, "
-                   f"{nq}q/{nkv}kv d{d} ctx {L}: 1 run single-threaded, {reps} runs on "
+        "sample": (f"reference CPU fused attention (fused_attention.ea two-pass, extended "
+                   f"to GQA), {what}: 1 sequence x 1 layer, {nq}q/{nkv}kv d{d} ctx {L}; "
+                   f"single-threaded median of {n1} runs after a warmup; {reps} runs on "
                    f"{threads} threads; scaled x{cfg['nseq']} sequences per layer"),
     }
 

@@ -108,6 +108,16 @@ void orc_fused_attention(int head_dim, const float *q,
                          float *out, int seq_len, int n_q_heads,
                          int n_kv_heads, int64_t groups_per_head);
 
+/* The same on AVX-512 (eakv_oracle_avx512.c): the reference's fused kernel
+ * as its compiler emits it, 16 lanes per instruction, bit-identical to
+ * orc_fused_attention.  Call only where orc_avx512_available() is nonzero. */
+int  orc_avx512_available(void);
+void orc_fused_attention_avx512(int head_dim, const float *q,
+                                const uint8_t *kw, const float *ks, const float *kb,
+                                const uint8_t *vw, const float *vs, const float *vb,
+                                float *out, int seq_len, int n_q_heads,
+                                int n_kv_heads, int64_t groups_per_head);
+
 /* Row softmax between K-score and V-sum (the caller's step; HOWTO.md:52),
  * defined like the fused kernel: m = max(-1e6, row), w = expf(s-m),
  * sequential sum, w *= 1/sum. */
@@ -137,6 +147,9 @@ void orc_attention_output(const orc_cache_t *c, const float *weights,
 void orc_attention_fused(const orc_cache_t *c, const float *queries,
                          int layer, int n_q_heads, int n_kv_heads,
                          float *output_out);
+void orc_attention_fused_avx512(const orc_cache_t *c, const float *queries,
+                                int layer, int n_q_heads, int n_kv_heads,
+                                float *output_out);
 int  orc_cache_seq_len(const orc_cache_t *c);
 int  orc_cache_n_layers(const orc_cache_t *c);
 int  orc_cache_n_heads(const orc_cache_t *c);

@@ -48,6 +48,8 @@ _SIG = {
     "orc_attention_scores": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "orc_attention_output": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "orc_attention_fused": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "orc_attention_fused_avx512": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "orc_avx512_available": (C.c_int, []),
     "orc_cache_seq_len": (C.c_int, [_vp]),
     "orc_cache_n_layers": (C.c_int, [_vp]),
     "orc_cache_n_heads": (C.c_int, [_vp]),
@@ -203,6 +205,11 @@ def v_sum(head_dim, wts, w, s, b, seq_len, n_q, n_kv, gph):
     return out
 
 
+def avx512_available():
+    """Whether this CPU runs the AVX-512 restatement of the fused kernel."""
+    return bool(lib().orc_avx512_available())
+
+
 def softmax_rows(scores):
     sc = _f32(scores)
     n, L = sc.shape
@@ -289,6 +296,16 @@ class OracleCache:
         q = _f32(q)
         out = np.zeros((n_q, self.head_dim), np.float32)
         lib().orc_attention_fused(self.h, _p(q), layer, n_q, n_kv, _p(out))
+        return out
+
+    def attention_fused_avx512(self, q, layer, n_q, n_kv):
+        """orc_attention_fused on AVX-512 (bit-identical); needs
+        avx512_available()."""
+        if not avx512_available():
+            raise RuntimeError("this CPU lacks AVX-512 (F, BW, DQ, VL)")
+        q = _f32(q)
+        out = np.zeros((n_q, self.head_dim), np.float32)
+        lib().orc_attention_fused_avx512(self.h, _p(q), layer, n_q, n_kv, _p(out))
         return out
 
     def read_planes(self, layer, kv_idx):

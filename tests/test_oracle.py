@@ -247,6 +247,22 @@ def test_fused_empty_context_is_nan():
     assert np.isnan(out).all()
 
 
+@pytest.mark.skipif(not O.avx512_available(), reason="this CPU lacks AVX-512")
+@pytest.mark.parametrize("d,n_q,n_kv,L", [(128, 32, 8, 700), (64, 8, 4, 300), (128, 4, 4, 1),
+                                          (64, 16, 2, 65), (128, 6, 2, 0)])
+def test_avx512_fused_attention_is_the_scalar_one(rng, d, n_q, n_kv, L):
+    """The CPU baseline's AVX-512 form of the fused kernel (16-lane
+    intrinsics) does the scalar restatement's arithmetic lane for lane:
+    equal bit for bit, NaN for NaN (empty context)."""
+    c = O.OracleCache(1, n_kv, d, max(L, 1) + 3)
+    if L:
+        c.load_raw((rng.standard_normal((1, 2, n_kv, L, d)) * 2).astype(np.float32), L)
+    q = (rng.standard_normal((n_q, d)) * 1.5).astype(np.float32)
+    a = c.attention_fused(q, 0, n_q, n_kv)
+    b = c.attention_fused_avx512(q, 0, n_q, n_kv)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 # ------------------------------------------------- dequantize range, validate
 
 def test_dequantize_range_is_a_slice_of_the_closed_form(rng):
