@@ -399,8 +399,8 @@ struct WaveState {
 // given (q points to w[n_q][L] of one sequence).  No K, no softmax: each
 // tile's weights are loaded in place of its K bytes and go straight to the
 // digit rows (signed fixed point, the exponent from the largest |a|); m
-// stays 0, the merge adds the chunks unnormalised, and a non-finite weight
-// makes its head's output NaN (lsum carries the flag).
+// stays 0, vsum_merge_kernel adds the chunks unnormalised, and a non-finite
+// weight makes its head's output NaN (lsum carries the flag).
 template <int D, int HH, bool VS>
 __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, HH> / 4)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
@@ -999,14 +999,13 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
 
 // Merge of the MFMA program's chunk partials (log2 domain) per (q head,
 // sequence): M = max(-1e6 log2(e), m_c) (the reference's max starts at
-// -1e6), l = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M), out = o * (1/l)
-// (V-sum: out = o).
+// -1e6), l = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M), out = o * (1/l).
 // The chunks are read kMergeBatch at a time with all loads in flight and
 // merged online across batches.  An empty sequence has no chunks:
 // 0 * (1/0) = NaN, as the reference.
 constexpr int kMergeBatch = 16;
 
-template <int D, bool VS>
+template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(
     eakvd_batch bt, int n_q, int max_chunks, int wpb, const float *__restrict__ part,
     float *__restrict__ out)
@@ -1041,10 +1040,57 @@ __global__ __launch_bounds__(D) void merge_kernel(
         }
         M = Mn;
     }
-    // V-sum: the plain sum (m = 0 in every chunk); lt is 0, or NaN after a
-    // non-finite weight
-    if constexpr (VS) out[((int64_t)s * n_q + qh) * D + i] = lt == lt ? ot : lt;
-    else out[((int64_t)s * n_q + qh) * D + i] = ot * (1.0f / lt);
+    out[((int64_t)s * n_q + qh) * D + i] = ot * (1.0f / lt);
+}
+
+// V-sum mode's merge: out[qh][i] = the plain sum over chunks of the
+// partials' o[i] (every chunk's m is 0), in a fixed order: a block takes 32
+// dims of one q head; thread (i, part) adds chunks part, part + 8, ...,
+// kVsBatch at a time with their loads in flight, and the 8 part sums are
+// added in part order.  A chunk whose l is NaN (a non-finite weight) makes
+// the head's outputs NaN.
+constexpr int kVsParts = 8;
+constexpr int kVsBatch = 16;
+
+template <int D>
+__global__ __launch_bounds__(256) void vsum_merge_kernel(int stride, int n_chunks,
+                                                         const float *__restrict__ part,
+                                                         float *__restrict__ out)
+{
+    __shared__ float red[kVsParts][32];
+    __shared__ float flag[kVsParts];
+    const int qh = blockIdx.x / (D / 32), i = (blockIdx.x % (D / 32)) * 32 + (threadIdx.x & 31);
+    const int pt = threadIdx.x >> 5;
+    const float *p = part + (int64_t)qh * stride * (D + 2);    // stride: chunks per head
+    float sum = 0.0f, bad = 0.0f;
+    for (int c0 = pt; c0 < n_chunks; c0 += kVsParts * kVsBatch) {
+        float o[kVsBatch], l[kVsBatch];
+#pragma unroll
+        for (int j = 0; j < kVsBatch; j++) {
+            const int c = min(c0 + j * kVsParts, n_chunks - 1);
+            o[j] = p[(int64_t)c * (D + 2) + 2 + i];
+            l[j] = p[(int64_t)c * (D + 2) + 1];
+        }
+#pragma unroll
+        for (int j = 0; j < kVsBatch; j++)
+            if (c0 + j * kVsParts < n_chunks) {
+                sum = __fadd_rn(sum, o[j]);
+                bad = bad + l[j];                 // 0, or NaN after a non-finite weight
+            }
+    }
+    red[pt][threadIdx.x & 31] = sum;
+    if ((threadIdx.x & 31) == 0) flag[pt] = bad;
+    __syncthreads();
+    if (pt == 0) {
+        float t = red[0][threadIdx.x];
+        float f = flag[0];
+#pragma unroll
+        for (int k = 1; k < kVsParts; k++) {
+            t = __fadd_rn(t, red[k][threadIdx.x]);
+            f = f + flag[k];
+        }
+        out[(int64_t)qh * D + i] = f == f ? t : f;
+    }
 }
 
 // ------------------------------------------------------------------ VALU
@@ -1290,11 +1336,11 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, qpk, rs,
                            part);
         if (g->head_dim == 64)
-            hipLaunchKernelGGL((merge_kernel<64, false>), mgrid, dim3(64), 0, st, *b, n_q, mc,
-                               wpb, part, out);
+            hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc, wpb,
+                               part, out);
         else
-            hipLaunchKernelGGL((merge_kernel<128, false>), mgrid, dim3(128), 0, st, *b, n_q, mc,
-                               wpb, part, out);
+            hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc, wpb,
+                               part, out);
         return (int)hipGetLastError();
     }
     const int mc = (ml + kChunkV - 1) / kChunkV;
@@ -1350,18 +1396,20 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
     const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
     const int mc = mfma_blocks_per_unit(seq_len, n_kv, per_cu);
     const dim3 grid((unsigned)mc, (unsigned)n_kv, 1u);
-    const dim3 mgrid((unsigned)n_q, 1u);
     float *part = (float *)work;
     auto kern = g->head_dim == 64
                     ? (hh == 1 ? mfma_kernel<64, 1, true> : mfma_kernel<64, 2, true>)
                     : (hh == 1 ? mfma_kernel<128, 1, true> : mfma_kernel<128, 2, true>);
     hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, b, layer, w, n_q, qpk, 0.0f,
                        part);
+    // the chunks that hold a partial: blocks with a tile (see mfma_kernel)
+    const int n_tiles = (seq_len + kTT - 1) / kTT;
+    const int nch = min(mc, (n_tiles + wpb - 1) / wpb);
     if (g->head_dim == 64)
-        hipLaunchKernelGGL((merge_kernel<64, true>), mgrid, dim3(64), 0, st, b, n_q, mc, wpb,
-                           part, out);
+        hipLaunchKernelGGL(vsum_merge_kernel<64>, dim3((unsigned)(n_q * 2)), dim3(256), 0, st,
+                           mc, nch, part, out);
     else
-        hipLaunchKernelGGL((merge_kernel<128, true>), mgrid, dim3(128), 0, st, b, n_q, mc, wpb,
-                           part, out);
+        hipLaunchKernelGGL(vsum_merge_kernel<128>, dim3((unsigned)(n_q * 4)), dim3(256), 0, st,
+                           mc, nch, part, out);
     return (int)hipGetLastError();
 }
