@@ -96,8 +96,9 @@ size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len, int n_q);
 int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base, int layer,
                 int seq_len, const float *w, int n_q, int n_kv, float *out,
                 void *work, void *stream);
-/* The same on the matrix cores (hip/fused.hip), for 2 to 8 q heads per kv
- * head; returns -1 without launching anything where it does not apply.
+/* The same on the matrix cores (hip/fused.hip), for 2 or more q heads per
+ * kv head (above 8 as virtual kv heads of at most 8); returns -1 without
+ * launching anything where it does not apply.
  * eakvd_v_sum tries it first. */
 size_t eakvd_v_sum_mfma_work_bytes(const eakvd_geom *g, int seq_len, int n_q);
 int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int layer,

@@ -12,8 +12,10 @@
 //
 // Two block programs:
 //
-// mfma_kernel (up to 4 q heads per kv head): 4 waves, each walking 32-token
-//   tiles with two pipeline stages in flight.  Both products run on the int8
+// mfma_kernel (one or two quads of q heads per wave: up to 8 q heads per kv
+//   head; larger groups as virtual kv heads of at most 8 that share the kv
+//   head's tiles; also the unfused V-sum): waves walking 32-token tiles with
+//   two pipeline stages in flight.  Both products run on the int8
 //   matrix cores; on gfx950 matrix and vector instructions of a SIMD do not
 //   overlap, so the design minimises their sum:
 //   K: per 16 tokens and 64-dim group one v_mfma_i32_16x16x64_i8, A = the q
@@ -31,8 +33,10 @@
 //     exchanged through LDS the same way.  sum p*bias per (head, group) is
 //     kept apart and added at the end.
 //   Waves are merged in LDS, chunks by merge_kernel.
-// valu_kernel (wider groups): one lane per token for K with the reference
-//   arithmetic, then V by dims; same partial/merge scheme.
+// valu_kernel (group sizes above 8 with no split into parts of at most 8,
+//   e.g. 11, and planes beyond 32-bit buffer offsets): one lane per token for
+//   K with the reference arithmetic, then V by dims; same partial/merge
+//   scheme.
 #include <string.h>
 
 #include <type_traits>
@@ -404,7 +408,7 @@ struct WaveState {
 template <int D, int HH, bool VS>
 __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, HH> / 4)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
-    int n_q, int qpk, float rs, float *__restrict__ part)
+    int n_q, int qpk, float rs, float *__restrict__ part, int split)
 {
     constexpr int GPD = D / 64;
     constexpr int NK = Geo<D>::NK;
@@ -449,7 +453,9 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     const int stride = nb * NW;                         // tiles between its tiles
     const Planes K = planes_of(g, bt.base[s], layer, 0);
     const Planes V = planes_of(g, bt.base[s], layer, 1);
-    const int64_t hbase = (int64_t)kvh * g.gph;
+    // split > 1: blockIdx.y is one of `split` virtual kv heads of qpk q heads
+    // each that share kv head kvh / split (more than 8 q heads per kv head)
+    const int64_t hbase = (int64_t)(kvh / split) * g.gph;
     const float *qs = q + ((int64_t)s * n_q + (int64_t)kvh * qpk) * D;
 
     // ---- q -> A operands of K.  Lane l: row i = l%16 (head ha = i/4, digit
@@ -1293,6 +1299,17 @@ int mfma_blocks_per_unit(int ml, int units, int per_cu)
     return nb < 1 ? 1 : nb;
 }
 
+// Virtual kv heads per kv head for the MFMA program: 1 up to 8 q heads per
+// kv head; above, the fewest that divide the group into parts of at most 8
+// (each part reads the kv head's tiles again, through L2); 0 if none does.
+int mfma_split(int qpk)
+{
+    if (qpk <= 8) return 1;
+    for (int sp = 2; sp <= qpk; sp++)
+        if (qpk % sp == 0 && qpk / sp <= 8) return sp;
+    return 0;
+}
+
 int max_len(const eakvd_batch *b)
 {
     int mx = 0;
@@ -1322,19 +1339,21 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
     // the MFMA program addresses a layer's K and V blocks with 32-bit buffer
     // offsets
     const bool small_planes = 2 * g->block_bytes <= (int64_t)0x7fffffff;
-    if (qpk <= 8 && small_planes) {
-        const int hh = qpk <= 4 ? 1 : 2;
+    const int split = mfma_split(qpk);
+    if (split > 0 && small_planes) {
+        const int qv = qpk / split;                         // q heads per virtual kv head
+        const int hh = qv <= 4 ? 1 : 2;
         const int per_cu = g->head_dim == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
                                              : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
         const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
-        const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv, per_cu);
-        const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
+        const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv * split, per_cu);
+        const dim3 grid((unsigned)mc, (unsigned)(n_kv * split), (unsigned)b->n_seq);
         const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
         auto kern = g->head_dim == 64
                         ? (hh == 1 ? mfma_kernel<64, 1, false> : mfma_kernel<64, 2, false>)
                         : (hh == 1 ? mfma_kernel<128, 1, false> : mfma_kernel<128, 2, false>);
-        hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, qpk, rs,
-                           part);
+        hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, qv, rs,
+                           part, split);
         if (g->head_dim == 64)
             hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc, wpb,
                                part, out);
@@ -1363,13 +1382,14 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
     return (int)hipGetLastError();
 }
 
-// The unfused V-sum on the matrix cores (mfma_kernel in V-sum mode) for 2 to
-// 8 q heads per kv head: out[n_q][D] = sum_t w[h][t] V[t] over seq_len
-// tokens of one cache, the chunk partials in `work`.  Returns -1 (nothing
-// launched) where it does not apply: MHA (one q head per kv head fills a
-// quarter of each MFMA; the VALU kernel measured as fast or faster there),
-// more than 8 q heads per kv head, planes beyond 32-bit buffer offsets, or
-// weights beyond 2 GiB.
+// The unfused V-sum on the matrix cores (mfma_kernel in V-sum mode) for 2 or
+// more q heads per kv head (above 8 as virtual kv heads, see mfma_split):
+// out[n_q][D] = sum_t w[h][t] V[t] over seq_len tokens of one cache, the
+// chunk partials in `work`.  Returns -1 (nothing launched) where it does not
+// apply: MHA (one q head per kv head fills a quarter of each MFMA; the VALU
+// kernel measured as fast or faster there), a group size with no split into
+// parts of at most 8, planes beyond 32-bit buffer offsets, or weights beyond
+// 2 GiB.
 extern "C" size_t eakvd_v_sum_mfma_work_bytes(const eakvd_geom *g, int seq_len, int n_q)
 {
     const int mc = (seq_len + kChunkV - 1) / kChunkV;
@@ -1381,27 +1401,29 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
                                 void *work, void *stream)
 {
     const int qpk = n_q / n_kv;
-    if (qpk < 2 || qpk > 8 || 2 * g->block_bytes > (int64_t)0x7fffffff ||
+    const int split = qpk < 2 ? 0 : mfma_split(qpk);
+    if (split == 0 || 2 * g->block_bytes > (int64_t)0x7fffffff ||
         (int64_t)qpk * seq_len * 4 > (int64_t)0x7fffffff || seq_len <= 0)
         return -1;
+    const int qv = qpk / split;                             // q heads per virtual kv head
     const hipStream_t st = (hipStream_t)stream;
     eakvd_batch b;
     memset(&b, 0, sizeof(b));
     b.n_seq = 1;
     b.base[0] = base;
     b.seq_len[0] = seq_len;
-    const int hh = qpk <= 4 ? 1 : 2;
+    const int hh = qv <= 4 ? 1 : 2;
     const int per_cu = g->head_dim == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
                                          : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
     const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
-    const int mc = mfma_blocks_per_unit(seq_len, n_kv, per_cu);
-    const dim3 grid((unsigned)mc, (unsigned)n_kv, 1u);
+    const int mc = mfma_blocks_per_unit(seq_len, n_kv * split, per_cu);
+    const dim3 grid((unsigned)mc, (unsigned)(n_kv * split), 1u);
     float *part = (float *)work;
     auto kern = g->head_dim == 64
                     ? (hh == 1 ? mfma_kernel<64, 1, true> : mfma_kernel<64, 2, true>)
                     : (hh == 1 ? mfma_kernel<128, 1, true> : mfma_kernel<128, 2, true>);
-    hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, b, layer, w, n_q, qpk, 0.0f,
-                       part);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, b, layer, w, n_q, qv, 0.0f,
+                       part, split);
     // the chunks that hold a partial: blocks with a tile (see mfma_kernel)
     const int n_tiles = (seq_len + kTT - 1) / kTT;
     const int nch = min(mc, (n_tiles + wpb - 1) / wpb);

@@ -224,6 +224,27 @@ def test_v_sum_signed_and_nonfinite_weights(E, rng, nh, n_q, n_kv, d, L, lmax):
     assert np.all(err <= 1e-4 + 4e-7 * mag[keep]), err.max()
 
 
+@pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", [
+    (2, 32, 2, 128, 1500, 1500), (1, 16, 1, 64, 2100, 2100), (2, 24, 2, 128, 700, 704),
+    (2, 20, 2, 64, 333, 340), (1, 11, 1, 128, 500, 500), (4, 48, 4, 128, 1025, 1030)])
+def test_large_groups_fused_and_v_sum(E, rng, nh, n_q, n_kv, d, L, lmax):
+    """More than 8 q heads per kv head (MQA and wide GQA): the matrix-core
+    programs split the group into virtual kv heads of at most 8 q heads that
+    read the same kv head (16 -> 2 x 8, 24 -> 3 x 8, 10 -> 2 x 5, 12 -> 2 x 6);
+    11 has no such split and runs the VALU programs.  Fused attention and
+    the V-sum against the oracle."""
+    say("large-groups", nh, n_q, n_kv, d, L)
+    g, o = loaded(E, rng, nh, d, L, lmax)
+    q = (rng.standard_normal((n_q, d)) * 2).astype(np.float32)
+    ok, err, nbad = tol_close(g.attention_fused(q, 1, n_q, n_kv),
+                              o.attention_fused(q, 1, n_q, n_kv), ATOL, RTOL)
+    assert ok, (err, nbad)
+    w = O.softmax_rows(o.attention_scores(q, 1, n_q, n_kv))
+    ok, err, nbad = tol_close(g.attention_output(w, 1, n_q, n_kv),
+                              o.attention_output(w, 1, n_q, n_kv), ATOL, RTOL)
+    assert ok, (err, nbad)
+
+
 @pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", SHAPES)
 def test_fused_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
     say("fused", nh, n_q, n_kv, d, L)
