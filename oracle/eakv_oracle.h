@@ -1,8 +1,8 @@
 /* eakv_oracle.h — CPU restatement of the reference eakv hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker that the HIP library is
- * compared against; it is never linked into, loaded by or called from the
- * product library.  Only tests/, __graft_entry__.smoke() and the CPU-baseline
+ * TEST INFRASTRUCTURE ONLY.  This is the oracle that the HIP library's
+ * results are compared against; it is never linked into, loaded by or called
+ * from the product library.  Only tests/, __graft_entry__.smoke() and the CPU-baseline
  * leg of bench.py may load it.
  *
  * Every function restates the arithmetic of one reference kernel (Ea source,

@@ -1,7 +1,8 @@
 """ctypes binding of the CPU oracle (liboracle.so) — TEST INFRASTRUCTURE ONLY.
 
 Loaded by tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg as
-the checker; never by the eakv_amd package.  ``OracleCache`` offers the same
+the oracle the HIP results are compared against; never by the eakv_amd
+package.  ``OracleCache`` offers the same
 methods as ``eakv_amd.Cache`` so one test body can drive either.
 """
 from __future__ import annotations
