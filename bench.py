@@ -345,6 +345,84 @@ def dequant_bench(w, steps, warmup):
                          "alg_bytes_per_launch": alg}}
 
 
+def validate_bench(w, steps, warmup):
+    """The integrity check (eakv_validate) of the first cache: every (layer,
+    kv) block's scales and biases over the groups the reference checks, 8 B
+    read per group.  eakv_validate returns when its codes are on the host, so
+    this times the whole call (host clock): one kernel, a 0xff fill of the
+    per-block results and their copy back."""
+    E, c = w.E, w.cfg
+    cache = w.caches[0]
+    res = np.zeros(2 * c["nl"], np.int32)
+    L = E.lib()
+    for _ in range(warmup):
+        assert L.eakv_validate(cache.h, res.ctypes.data) == 0, E.last_error()
+    t = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        assert L.eakv_validate(cache.h, res.ctypes.data) == 0, E.last_error()
+        t.append(time.perf_counter() - t0)
+    us = float(np.median(t)) * 1e6
+    n = c["nkv"] * c["d"] * cache.seq_len // 64
+    alg = 2 * c["nl"] * n * 8
+    gbs = alg / (us * 1e-6) / 1e9
+    return {"metric": "integrity check GB/s (scale + bias read per group, whole host call)",
+            "value": round(gbs, 1), "unit": "GB/s", "higher_is_better": True,
+            "us_per_call": round(us, 1), "groups_per_block": n, "blocks": 2 * c["nl"],
+            "codes": res.tolist()[:4], "steps": steps, "n_gpus": 1, "dtype": "f32 bit tests",
+            "config": {"workload": c["name"]},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "alg_bytes_per_call": alg}}
+
+
+def ggml_bench(steps, warmup, n_rows=65536, k=4096):
+    """The ggml block type's device functions on n_rows rows of k f32 values
+    (block_q4_1_eakv, 40 B per 64 values): quantize (4 B read + 0.625 B
+    written per value), dequantize (0.625 + 4), vec_dot of every row with
+    its own f32 row (0.625 + 4 read per value + 4 B per row), each one launch
+    over all rows, timed with HIP events."""
+    import eakv_amd as E
+    from eakv_amd import hipmem as H
+    L = E.lib()
+    n = n_rows * k
+    x = H.DeviceArray((n,))
+    Synth().fill(x.ptr, n_rows, 1, k, SEED_BASE, 0, 0, "normal")
+    y = H.DeviceArray((n,))
+    Synth().fill(y.ptr, n_rows, 1, k, SEED_BASE + 1, 0, 0, "normal")
+    blocks = H.DeviceArray((n // 64 * 40 // 4,))
+    deq = H.DeviceArray((n,))
+    s = H.DeviceArray((n_rows,))
+    row_b = k // 64 * 40
+    calls = {
+        "quantize_row": (lambda: L.eakv_ggml_quantize_row_device(x.ptr, blocks.ptr, n, None),
+                         n * 4 + n // 64 * 40),
+        "dequantize_row": (lambda: L.eakv_ggml_dequantize_row_device(blocks.ptr, deq.ptr, n, None),
+                           n // 64 * 40 + n * 4),
+        "vec_dot": (lambda: L.eakv_ggml_vec_dot_device(k, s.ptr, 4, blocks.ptr, row_b, y.ptr,
+                                                       k * 4, n_rows, None),
+                    n // 64 * 40 + n * 4 + n_rows * 4),
+    }
+    res = {}
+    for name, (call, alg) in calls.items():
+        for _ in range(warmup):
+            assert call() == 0, E.last_error()
+        H.synchronize()
+        e0, e1 = H.Event(), H.Event()
+        e0.record(None)
+        for _ in range(steps):
+            assert call() == 0, E.last_error()
+        e1.record(None)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / steps
+        gbs = alg / (us * 1e-6) / 1e9
+        res[name] = {"us_per_call": round(us, 2), "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes_per_call": alg}
+    return {"metric": "ggml block type device functions, GB/s of algorithmic bytes",
+            "unit": "GB/s", "n_gpus": 1, "steps": steps, "dtype": "block_q4_1_eakv <-> f32",
+            "config": {"rows": n_rows, "k": k, "bytes_f32": n * 4}, **res}
+
+
 def unfused_bench(w, steps, warmup):
     """The reference API's unfused path on the first cache, every layer back
     to back: eakv_attention_scores_device (k_score_kernel), then
@@ -418,6 +496,12 @@ def main():
     ap.add_argument("--dequant", action="store_true",
                     help="only time whole-plane dequantization of the first cache, "
                          "print its JSON line, then exit")
+    ap.add_argument("--validate", action="store_true",
+                    help="only time the integrity check of the first cache, print its "
+                         "JSON line, then exit")
+    ap.add_argument("--ggml", action="store_true",
+                    help="only time the ggml block type's device functions on 1 GiB of "
+                         "f32 rows, print their JSON line, then exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB, 5 times (the "
                          "known-size kernel for HBM byte counters), then exit")
@@ -428,6 +512,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration << 20)
+        return
+    if args.ggml:
+        print(json.dumps(ggml_bench(max(1, args.steps), 2)), flush=True)
         return
 
     from eakv_amd import hipmem as H
@@ -440,6 +527,9 @@ def main():
     H.synchronize()
     if args.dequant:
         print(json.dumps(dequant_bench(w, max(1, args.steps // 4), 1)), flush=True)
+        return
+    if args.validate:
+        print(json.dumps(validate_bench(w, max(3, args.steps), 2)), flush=True)
         return
     if args.unfused:
         print(json.dumps(unfused_bench(w, max(1, args.steps // 4), 1)), flush=True)

@@ -66,14 +66,28 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint8_t *__restrict
     const int32_t *sb = (const int32_t *)(blk + s_off);
     const int32_t *bb = (const int32_t *)(blk + b_off);
     unsigned long long key = ~0ull;
-    const int64_t step = (int64_t)gridDim.x * 256;
-    for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < n; g += step) {
-        const int32_t s = sb[g], b = bb[g];
+    auto check = [&](int64_t g, int32_t s, int32_t b) {
         const int code = nan_bits(s) ? 1 : nan_bits(b) ? 2 : __int_as_float(s) < 0.0f ? 3 : 0;
         if (code) {
             const unsigned long long k = (unsigned long long)g * 4 + (unsigned long long)code;
             key = k < key ? k : key;
         }
+    };
+    // four groups per lane and iteration, as 16-byte loads (the planes are
+    // 256-byte aligned); the last n % 4 groups one at a time
+    const int64_t n4 = n / 4;
+    const int64_t step = (int64_t)gridDim.x * 256;
+    for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < n4; j += step) {
+        const int4 s = reinterpret_cast<const int4 *>(sb)[j];
+        const int4 b = reinterpret_cast<const int4 *>(bb)[j];
+        check(4 * j, s.x, b.x);
+        check(4 * j + 1, s.y, b.y);
+        check(4 * j + 2, s.z, b.z);
+        check(4 * j + 3, s.w, b.w);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+        const int64_t g = 4 * n4 + threadIdx.x;
+        check(g, sb[g], bb[g]);
     }
     // the block's minimum: across the wave, then the waves
     for (int off = 32; off > 0; off >>= 1) {
@@ -116,7 +130,7 @@ extern "C" int eakvd_validate(const eakvd_geom *g, const uint8_t *base, int n_bl
                                   (hipStream_t)stream);
     if (e != hipSuccess) return (int)e;
     if (n <= 0 || n_blocks <= 0) return 0;
-    const int gx = grid_for(n) < 64 ? grid_for(n) : 64;
+    const int gx = grid_for((n + 3) / 4) < 64 ? grid_for((n + 3) / 4) : 64;
     hipLaunchKernelGGL(validate_kernel, dim3(gx, n_blocks), dim3(256), 0, (hipStream_t)stream,
                        base, g->block_bytes, g->s_off, g->b_off, n, res);
     return (int)hipGetLastError();
