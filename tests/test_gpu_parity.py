@@ -357,6 +357,30 @@ def test_fused_huge_scores_as_accurate_as_reference(E, rng, d, n_q, n_kv, L, slo
     assert e_gpu <= 2 * e_ref + 1e-5
 
 
+@pytest.mark.parametrize("d,n_q,n_kv,L,where", [(128, 32, 8, 700, "k"), (128, 16, 2, 300, "v"),
+                                                (64, 8, 4, 500, "k"), (128, 64, 8, 450, "v")])
+def test_fused_nonfinite_cache_values_propagate(E, rng, d, n_q, n_kv, L, where):
+    """A NaN as the first value of a 64-value group quantizes to a NaN scale
+    and bias (the strict min/max scan keeps it).  In K it makes that token's
+    score NaN and so every output of the kv head's q heads; in V it makes the
+    group's 64 output dims NaN.  The NaN pattern equals the oracle's and the
+    other values match it."""
+    say("fused-nan", d, n_q, n_kv, L, where)
+    data = rng.standard_normal((1, 2, n_kv, L, d)).astype(np.float32)
+    data[0, 0 if where == "k" else 1, 1, L // 3, 0] = np.nan
+    g, o = pair(E, 1, n_kv, d, L + 4)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    q = rng.standard_normal((n_q, d)).astype(np.float32)
+    a = g.attention_fused(q, 0, n_q, n_kv)
+    b = o.attention_fused(q, 0, n_q, n_kv)
+    nan = np.isnan(b)
+    assert nan.any() and not nan.all()
+    assert np.array_equal(np.isnan(a), nan)
+    ok, err, nbad = tol_close(a[~nan], b[~nan], ATOL, RTOL)
+    assert ok, (err, nbad)
+
+
 def test_fused_batch_device(E, rng):
     from eakv_amd.hipmem import DeviceArray
     nl, nh, d, n_q, lmax = 2, 4, 128, 16, 1100
