@@ -216,16 +216,14 @@ __device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int 
                                              (int)ss, 0, 0);
 }
 
-// Loads per group, in issue order: V chunks, scales, K bytes (fixed by sched
-// barriers).  The compiler does not order LDS reads after buffer loads to
+// Loads per group, in issue order: V chunks, scales, then the K bytes (or
+// the V-sum's weights; fixed by sched barriers).  The compiler does not order LDS reads after buffer loads to
 // LDS, so reads of a slot are preceded by an explicit wait for every load
 // older than the ones that may still be outstanding.
 template <int D>
 constexpr int kDma = 1;                                  // scale loads
 template <int D>
 constexpr int kNK = Geo<D>::NK * (D / 64);               // K loads
-template <int D>
-constexpr int kGroup = Geo<D>::NVD + kDma<D> + kNK<D>;   // loads per group
 
 // s_waitcnt vmcnt(n), no wait on the other counters (gfx9 encoding:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -394,10 +392,11 @@ struct WaveState {
 // wave sees.  Each block writes its partial (m, l, o[D]) per q head of its
 // kv head; merge_kernel combines the blocks.
 //
-// A wave serves the G = qpk <= 4 HH q heads of its kv head as HH quads of
-// four heads: each quad has its own q digits (K MFMA rows), softmax state,
-// digit rows and V MFMAs; the K bytes, the V tile in LDS and the nibbles
-// taken from them are shared, so the planes are read once for all G heads.
+// A wave serves the G = qpk <= 4 HH q heads of its (virtual) kv head as HH
+// quads of four heads: each quad has its own q digits (K MFMA rows), softmax
+// state, digit rows and V MFMAs; the K bytes, the V tile in LDS and the
+// nibbles taken from them are shared, so the planes are read once for all G
+// heads (once per virtual kv head when a group above 8 is split).
 //
 // VS: the V-sum of the unfused API, o = sum_t w[h][t] v[t] with the weights
 // given (q points to w[n_q][L] of one sequence).  No K, no softmax: each
