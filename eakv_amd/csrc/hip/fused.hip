@@ -1048,6 +1048,73 @@ __global__ __launch_bounds__(D) void merge_kernel(
     out[((int64_t)s * n_q + qh) * D + i] = ot * (1.0f / lt);
 }
 
+// The same merge for more than kMergeBatch chunks (long contexts): a block
+// takes 32 dims of one (q head, sequence); thread (i, part) merges
+// chunks part, part + 8, ... online, kPartBatch at a time with their loads
+// in flight, and the 8 part results are merged in part order.  An empty
+// sequence has no chunks: 0 * (1/0) = NaN, as the reference.
+constexpr int kMergeParts = 8;
+constexpr int kPartBatch = 8;
+
+template <int D>
+__global__ __launch_bounds__(256) void merge_parts_kernel(
+    eakvd_batch bt, int n_q, int max_chunks, int wpb, const float *__restrict__ part,
+    float *__restrict__ out)
+{
+    __shared__ float pm[kMergeParts], pl[kMergeParts], po[kMergeParts][32];
+    const int qh = blockIdx.x / (D / 32), s = blockIdx.y;
+    const int i = (blockIdx.x % (D / 32)) * 32 + (threadIdx.x & 31), pt = threadIdx.x >> 5;
+    // blocks that had a tile (see mfma_kernel; wpb waves per block)
+    const int n_tiles = (bt.seq_len[s] + kTT - 1) / kTT;
+    const int n_chunks = min(max_chunks, (n_tiles + wpb - 1) / wpb);
+    const float *p = part + ((int64_t)s * n_q + qh) * max_chunks * (D + 2);
+    float M = -1000000.0f * EAKV_LOG2E, lt = 0.0f, ot = 0.0f;
+    for (int c0 = pt; c0 < n_chunks; c0 += kMergeParts * kPartBatch) {
+        float m[kPartBatch], lv[kPartBatch], ov[kPartBatch];
+#pragma unroll
+        for (int j = 0; j < kPartBatch; j++) {
+            const float *pc = p + min(c0 + j * kMergeParts, n_chunks - 1) * (D + 2);
+            m[j] = pc[0];
+            lv[j] = pc[1];
+            ov[j] = pc[2 + i];
+        }
+        float Mn = M;
+#pragma unroll
+        for (int j = 0; j < kPartBatch; j++)
+            if (c0 + j * kMergeParts < n_chunks) Mn = fmaxf(Mn, m[j]);
+        const float f = __builtin_amdgcn_exp2f(M - Mn);
+        lt *= f;
+        ot *= f;
+#pragma unroll
+        for (int j = 0; j < kPartBatch; j++) {
+            const float wj =
+                c0 + j * kMergeParts < n_chunks ? __builtin_amdgcn_exp2f(m[j] - Mn) : 0.0f;
+            lt = fmaf(lv[j], wj, lt);
+            ot = fmaf(ov[j], wj, ot);
+        }
+        M = Mn;
+    }
+    if ((threadIdx.x & 31) == 0) {
+        pm[pt] = M;
+        pl[pt] = lt;
+    }
+    po[pt][threadIdx.x & 31] = ot;
+    __syncthreads();
+    if (pt == 0) {
+        float Mt = pm[0];
+#pragma unroll
+        for (int k = 1; k < kMergeParts; k++) Mt = fmaxf(Mt, pm[k]);
+        float l = 0.0f, o = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kMergeParts; k++) {
+            const float f = __builtin_amdgcn_exp2f(pm[k] - Mt);
+            l = fmaf(pl[k], f, l);
+            o = fmaf(po[k][threadIdx.x], f, o);
+        }
+        out[((int64_t)s * n_q + qh) * D + i] = o * (1.0f / l);
+    }
+}
+
 // V-sum mode's merge: out[qh][i] = the plain sum over chunks of the
 // partials' o[i] (every chunk's m is 0), in a fixed order: a block takes 32
 // dims of one q head; thread (i, part) adds chunks part, part + 8, ...,
@@ -1360,12 +1427,21 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv * split, per_cu);
         const dim3 grid((unsigned)mc, (unsigned)(n_kv * split), (unsigned)b->n_seq);
         const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
+        // more than one batch of chunks: the merge spread over 8 parts
+        const bool parts = mc > kMergeBatch;
+        const dim3 pgrid((unsigned)(n_q * (g->head_dim / 32)), (unsigned)b->n_seq);
         auto kern = g->head_dim == 64
                         ? (hh == 1 ? mfma_kernel<64, 1, false> : mfma_kernel<64, 2, false>)
                         : (hh == 1 ? mfma_kernel<128, 1, false> : mfma_kernel<128, 2, false>);
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, qv, rs,
                            part, split);
-        if (g->head_dim == 64)
+        if (parts && g->head_dim == 64)
+            hipLaunchKernelGGL(merge_parts_kernel<64>, pgrid, dim3(256), 0, st, *b, n_q, mc,
+                               wpb, part, out);
+        else if (parts)
+            hipLaunchKernelGGL(merge_parts_kernel<128>, pgrid, dim3(256), 0, st, *b, n_q, mc,
+                               wpb, part, out);
+        else if (g->head_dim == 64)
             hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc, wpb,
                                part, out);
         else
