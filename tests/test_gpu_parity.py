@@ -402,6 +402,33 @@ def test_fused_batch_device(E, rng):
         assert ok, (lens[i], err, nbad)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_fused_batch_long_short_and_empty(E, rng, d):
+    """A batch whose longest sequence splits into more than 16 chunks (the
+    8-part chunk merge) beside short sequences with fewer chunks and an empty
+    one: each sequence merges only its own chunks, and the empty one gives
+    NaN, as the reference's 0 * (1/0)."""
+    from eakv_amd.hipmem import DeviceArray
+    nl, nh, n_q, lmax = 1, 2, 8, 4608
+    lens = [0, 5, 4600, 300]
+    gs, os_ = [], []
+    for L in lens:
+        g, o = pair(E, nl, nh, d, lmax) if L == 0 else loaded(E, rng, nh, d, L, lmax, nl)
+        gs.append(g)
+        os_.append(o)
+    q = rng.standard_normal((len(lens), n_q, d)).astype(np.float32)
+    dq = DeviceArray.from_host(q)
+    dout = DeviceArray((len(lens), n_q, d))
+    assert E.lib().eakv_attention_fused_batch_device(E.handles(gs), len(gs), 0, dq.ptr,
+                                                     n_q, nh, dout.ptr, None) == 0
+    gs[0].sync()
+    out = dout.download()
+    assert np.isnan(out[0]).all()
+    for i in range(1, len(lens)):
+        ok, err, nbad = tol_close(out[i], os_[i].attention_fused(q[i], 0, n_q, nh), ATOL, RTOL)
+        assert ok, (lens[i], err, nbad)
+
+
 def test_workspace_ordered_across_caller_streams(E, rng):
     """Device calls on two caller streams, back to back, share the cache's
     workspace (the fused chunk partials, the V-sum partials): each call waits
