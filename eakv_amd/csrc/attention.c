@@ -191,6 +191,10 @@ int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
         int e = eakvd_stream_sync(c0->stream);
         if (e) rc = eakvi_hip_fail(e, "fused_batch");
     }
+    /* the other caches' planes: after the device-pointer calls enqueued on
+     * their own streams (a device-side wait, only where there are such) */
+    for (int i = 1; rc == EAKV_OK && i < n_caches; i++)
+        rc = eakvi_order_before(caches[i], st);
     eakvd_batch b;
     memset(&b, 0, sizeof(b));
     b.n_seq = n_caches;

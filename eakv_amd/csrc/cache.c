@@ -123,6 +123,51 @@ int eakvi_work_end(eakv_cache_t *c, void *st)
     return EAKV_OK;
 }
 
+void *eakvi_stream_or_default(const eakv_cache_t *c, void *s)
+{
+    if (s) return s;
+    ((eakv_cache_t *)c)->own_async++;
+    return c->stream;
+}
+
+/* Record c's order event on `from`; every stream in to[0..n) (other than
+ * `from`) waits for it on the device.  If the event cannot be used, a host
+ * wait for `from` orders the same work. */
+static int order_wait(eakv_cache_t *c, void *from, void *const *to, int n)
+{
+    int e = c->order_event ? 0 : eakvd_event_create(&c->order_event);
+    if (!e) e = eakvd_event_record(c->order_event, from);
+    for (int i = 0; !e && i < n; i++)
+        if (to[i] != from) e = eakvd_stream_wait_event(to[i], c->order_event);
+    if (e) {
+        int e2 = eakvd_stream_sync(from);
+        if (e2) return eakvi_hip_fail(e2, "stream order");
+    }
+    return EAKV_OK;
+}
+
+int eakvi_order_before(eakv_cache_t *c, void *st)
+{
+    if (st == c->stream || c->own_async == 0 ||
+        (c->own_async == c->ordered_seq && c->ordered_to == st))
+        return EAKV_OK;
+    int rc = order_wait(c, c->stream, &st, 1);
+    if (rc == EAKV_OK) {
+        c->ordered_seq = c->own_async;
+        c->ordered_to = st;
+    }
+    return rc;
+}
+
+int eakvi_order_after(eakv_cache_t *const *caches, int n, void *st)
+{
+    void *to[EAKVD_MAX_BATCH];
+    int k = 0;
+    for (int i = 0; i < n && i < EAKVD_MAX_BATCH; i++)
+        if (caches[i]->stream != st) to[k++] = caches[i]->stream;
+    return k ? order_wait(caches[0], st, to, k) : EAKV_OK;
+}
+
 /* ------------------------------------------------------------------------ */
 /* lifecycle: reference src/cache.c:11-58                                    */
 
@@ -155,6 +200,9 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
     if (e) goto hip_fail;
     e = eakvd_stream_create(&c->stream);
     if (e) goto hip_fail;
+    /* created here so that ordering a batched call allocates nothing */
+    e = eakvd_event_create(&c->order_event);
+    if (e) goto hip_fail;
     e = eakvd_malloc((void **)&c->dev, c->dev_bytes);
     if (e) goto hip_fail;
     /* the reference calloc()s its planes (cache.c:33) */
@@ -166,6 +214,7 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
 hip_fail:
     eakvi_hip_fail(e, "cache_create");
     if (c->dev) eakvd_free(c->dev);
+    if (c->order_event) eakvd_event_destroy(c->order_event);
     if (c->stream) eakvd_stream_destroy(c->stream);
     free(c);
     return NULL;
@@ -179,6 +228,7 @@ void eakv_cache_free(eakv_cache_t *c)
     if (c->stream) eakvd_stream_sync(c->stream);
     if (c->work_on_caller) eakvd_event_sync(c->work_event);
     if (c->work_event) eakvd_event_destroy(c->work_event);
+    if (c->order_event) eakvd_event_destroy(c->order_event);
     if (c->work) eakvd_free(c->work);
     if (c->dev) eakvd_free(c->dev);
     if (c->stream) eakvd_stream_destroy(c->stream);
@@ -350,6 +400,14 @@ int eakv_append_batch_device(eakv_cache_t *const *caches, int n_caches,
     eakv_cache_t *c0 = caches[0];
     int prev, rc = eakvi_enter(c0, &prev);
     if (rc) return rc;
+    void *st = eakvi_stream_or_default(c0, stream);
+    /* the launch writes every cache: after their streams' earlier work */
+    for (int i = 0; rc == EAKV_OK && i < n_caches; i++)
+        rc = eakvi_order_before(caches[i], st);
+    if (rc) {
+        eakvi_leave(prev);
+        return rc;
+    }
     eakvd_quant_job job;
     memset(&job, 0, sizeof(job));
     job.src = d_data;
@@ -364,8 +422,10 @@ int eakv_append_batch_device(eakv_cache_t *const *caches, int n_caches,
         job.base[i] = caches[i]->dev;
         job.g_off[i] = (int64_t)caches[i]->seq_len * c0->geom.gpd;
     }
-    int e = eakvd_quantize(&c0->geom, &job, eakvi_stream_or_default(c0, stream));
+    int e = eakvd_quantize(&c0->geom, &job, st);
     if (e) rc = eakvi_hip_fail(e, "append_batch launch");
+    /* later work on each cache's own stream comes after the launch */
+    if (rc == EAKV_OK) rc = eakvi_order_after(caches, n_caches, st);
     eakvi_leave(prev);
     return rc;
 }

@@ -121,6 +121,10 @@ size_t eakvd_fused_work_bytes(const eakvd_geom *g, const eakvd_batch *b,
 int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
                 const float *q, int n_q, int n_kv, float *out, void *work,
                 void *stream);
+/* The bytes of partials that eakvd_fused writes and reads for this batch
+ * and head split (at most eakvd_fused_work_bytes()). */
+size_t eakvd_fused_launch_bytes(const eakvd_geom *g, const eakvd_batch *b,
+                                int n_q, int n_kv);
 
 /* ---- whole-plane kernels (hip/planes.hip)
  * eakvd_dequantize: groups [g0, g0 + n) of block (layer, kv) to out

@@ -1395,6 +1395,38 @@ int max_len(const eakvd_batch *b)
     return mx;
 }
 
+// The launch shape of one fused call: the matrix-core program (chunks per
+// unit mc, waves per block wpb, virtual kv heads per kv head split, q heads
+// per virtual head qv, quads hh) or the VALU program (mc chunks of kChunkV).
+struct FusedPlan {
+    bool mfma;
+    int mc, wpb, split, qv, hh;
+};
+
+FusedPlan fused_plan(const eakvd_geom *g, const eakvd_batch *b, int n_q, int n_kv)
+{
+    FusedPlan p{};
+    const int qpk = n_q / n_kv;
+    const int ml = max_len(b);
+    // the MFMA program addresses a layer's K and V blocks with 32-bit buffer
+    // offsets
+    const bool small_planes = 2 * g->block_bytes <= (int64_t)0x7fffffff;
+    p.split = mfma_split(qpk);
+    p.mfma = p.split > 0 && small_planes;
+    if (p.mfma) {
+        p.qv = qpk / p.split;
+        p.hh = p.qv <= 4 ? 1 : 2;
+        const int per_cu = g->head_dim == 64
+                               ? (p.hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
+                               : (p.hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
+        p.wpb = p.hh == 1 ? kWavesH<1> : kWavesH<2>;
+        p.mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv * p.split, per_cu);
+    } else {
+        p.mc = (ml + kChunkV - 1) / kChunkV;
+    }
+    return p;
+}
+
 }  // namespace
 
 extern "C" size_t eakvd_fused_work_bytes(const eakvd_geom *g,
@@ -1405,27 +1437,25 @@ extern "C" size_t eakvd_fused_work_bytes(const eakvd_geom *g,
     return (size_t)b->n_seq * n_q * mc * (g->head_dim + 2) * sizeof(float);
 }
 
+extern "C" size_t eakvd_fused_launch_bytes(const eakvd_geom *g, const eakvd_batch *b,
+                                           int n_q, int n_kv)
+{
+    // partial (m, l, o[D]) of every (sequence, q head, chunk)
+    const FusedPlan p = fused_plan(g, b, n_q, n_kv);
+    return (size_t)b->n_seq * n_q * p.mc * (g->head_dim + 2) * sizeof(float);
+}
+
 extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
                            int layer, const float *q, int n_q, int n_kv,
                            float *out, void *work, void *stream)
 {
     const hipStream_t st = (hipStream_t)stream;
-    const int qpk = n_q / n_kv;
     const float rs = 1.0f / sqrtf((float)g->head_dim);
     float *part = (float *)work;
-    const int ml = max_len(b);
-    // the MFMA program addresses a layer's K and V blocks with 32-bit buffer
-    // offsets
-    const bool small_planes = 2 * g->block_bytes <= (int64_t)0x7fffffff;
-    const int split = mfma_split(qpk);
-    if (split > 0 && small_planes) {
-        const int qv = qpk / split;                         // q heads per virtual kv head
-        const int hh = qv <= 4 ? 1 : 2;
-        const int per_cu = g->head_dim == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
-                                             : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
-        const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
-        const int mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv * split, per_cu);
-        const dim3 grid((unsigned)mc, (unsigned)(n_kv * split), (unsigned)b->n_seq);
+    const FusedPlan p = fused_plan(g, b, n_q, n_kv);
+    if (p.mfma) {
+        const int mc = p.mc, wpb = p.wpb, hh = p.hh;
+        const dim3 grid((unsigned)mc, (unsigned)(n_kv * p.split), (unsigned)b->n_seq);
         const dim3 mgrid((unsigned)n_q, (unsigned)b->n_seq);
         // more than one batch of chunks: the merge spread over 8 parts
         const bool parts = mc > kMergeBatch;
@@ -1433,8 +1463,8 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         auto kern = g->head_dim == 64
                         ? (hh == 1 ? mfma_kernel<64, 1, false> : mfma_kernel<64, 2, false>)
                         : (hh == 1 ? mfma_kernel<128, 1, false> : mfma_kernel<128, 2, false>);
-        hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, qv, rs,
-                           part, split);
+        hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, p.qv, rs,
+                           part, p.split);
         if (parts && g->head_dim == 64)
             hipLaunchKernelGGL(merge_parts_kernel<64>, pgrid, dim3(256), 0, st, *b, n_q, mc,
                                wpb, part, out);
@@ -1449,7 +1479,8 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
                                part, out);
         return (int)hipGetLastError();
     }
-    const int mc = (ml + kChunkV - 1) / kChunkV;
+    const int qpk = n_q / n_kv;
+    const int mc = p.mc;
     if (mc > 0) {
         const dim3 grid((unsigned)mc, (unsigned)n_kv, (unsigned)b->n_seq);
         if (g->head_dim == 64)

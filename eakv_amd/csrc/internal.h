@@ -28,6 +28,10 @@ struct eakv_cache {
     size_t work_bytes;
     void  *work_event;     /* recorded after a use of `work` on a caller's stream */
     int    work_on_caller; /* the last use of `work` was on a caller's stream */
+    void  *order_event;    /* orders a batched call against this cache's stream */
+    unsigned own_async;    /* device-pointer calls enqueued on `stream` so far */
+    unsigned ordered_seq;  /* own_async when a batched call last waited for `stream` */
+    void    *ordered_to;   /* the stream that waited */
 };
 
 /* error side channel (cache.c) */
@@ -47,9 +51,18 @@ int  eakvi_work_begin(eakv_cache_t *c, void *st, size_t n);
  * scratch's event there so that the next use waits for this one. */
 int  eakvi_work_end(eakv_cache_t *c, void *st);
 
-static inline void *eakvi_stream_or_default(const eakv_cache_t *c, void *s)
-{
-    return s ? s : c->stream;
-}
+/* Batched calls on stream st that name several caches:
+ * eakvi_order_before makes st wait, on the device, for the device-pointer
+ * calls enqueued so far on c's own stream (nothing when st is that stream or
+ * there are none since the last such wait by st; host-pointer calls finish
+ * before they return).  eakvi_order_after makes the own streams of caches
+ * [0, n) wait for the work enqueued so far on st (one event, recorded with
+ * caches[0]'s order_event). */
+int  eakvi_order_before(eakv_cache_t *c, void *st);
+int  eakvi_order_after(eakv_cache_t *const *caches, int n, void *st);
+
+/* The stream a device-pointer call runs on: the caller's, or (NULL) the
+ * cache's own, which the call then counts as pending work on it. */
+void *eakvi_stream_or_default(const eakv_cache_t *c, void *s);
 
 #endif

@@ -63,7 +63,10 @@ int eakv_cache_append_device(eakv_cache_t *cache, const float *d_data,
 /* Append n_tokens to every layer and both K/V of n_caches caches in one
  * launch.  d_data: f32[n_caches][n_layers][2][n_kv_heads][n_tokens][head_dim].
  * Caches must share n_layers, n_kv_heads, head_dim, max_seq_len and device;
- * seq_len is not changed (call eakv_cache_advance on each). */
+ * seq_len is not changed (call eakv_cache_advance on each).  The launch runs
+ * on `stream` (NULL: caches[0]'s own) after the device-pointer calls already
+ * enqueued on every named cache's own stream, and later work on those
+ * streams (host-pointer calls included) runs after it. */
 int eakv_append_batch_device(eakv_cache_t *const *caches, int n_caches,
                              const float *d_data, int n_tokens, void *stream);
 
@@ -85,7 +88,11 @@ int eakv_attention_fused(const eakv_cache_t *cache, const float *queries,
 
 /* Fused decode attention for n_caches same-shape caches (each over its own
  * seq_len) in one launch: d_q, d_out f32[n_caches][n_q][head_dim].  Uses the
- * workspace of caches[0]; a call counts as a use of every cache it names. */
+ * workspace of caches[0].  The launch runs on `stream` (NULL: caches[0]'s
+ * own) after the work already enqueued on every named cache's own stream
+ * (device-pointer calls there, e.g. an append with a NULL stream).  It only
+ * reads the other caches: work that later overwrites their tokens from
+ * another stream must wait for `stream` first. */
 int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
                                       int n_caches, int layer,
                                       const float *d_q, int n_q_heads,
