@@ -33,10 +33,10 @@
 //     exchanged through LDS the same way.  sum p*bias per (head, group) is
 //     kept apart and added at the end.
 //   Waves are merged in LDS, chunks by merge_kernel.
-// valu_kernel (group sizes above 8 with no split into parts of at most 8,
-//   e.g. 11, and planes beyond 32-bit buffer offsets): one lane per token for
-//   K with the reference arithmetic, then V by dims; same partial/merge
-//   scheme.
+// valu_kernel (caches whose (layer, kv) blocks are beyond the 32-bit buffer
+//   offsets of mfma_kernel, above 1 GiB; every group size has a split into
+//   virtual kv heads, at worst of one q head each): one lane per token for K
+//   with the reference arithmetic, then V by dims; same partial/merge scheme.
 #include <string.h>
 
 #include <type_traits>

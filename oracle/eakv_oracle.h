@@ -150,6 +150,16 @@ void orc_attention_fused(const orc_cache_t *c, const float *queries,
 void orc_attention_fused_avx512(const orc_cache_t *c, const float *queries,
                                 int layer, int n_q_heads, int n_kv_heads,
                                 float *output_out);
+/* eakv_attention_scores / eakv_attention_output of the oracle cache on
+ * AVX-512 (the reference's unfused kernels as the Ea compiler emits them),
+ * bit-identical to orc_attention_scores / orc_attention_output.  Call only
+ * where orc_avx512_available() is nonzero. */
+void orc_attention_scores_avx512(const orc_cache_t *c, const float *queries,
+                                 int layer, int n_q_heads, int n_kv_heads,
+                                 float *scores_out);
+void orc_attention_output_avx512(const orc_cache_t *c, const float *weights,
+                                 int layer, int n_q_heads, int n_kv_heads,
+                                 float *output_out);
 int  orc_cache_seq_len(const orc_cache_t *c);
 int  orc_cache_n_layers(const orc_cache_t *c);
 int  orc_cache_n_heads(const orc_cache_t *c);

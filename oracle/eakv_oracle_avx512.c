@@ -1,12 +1,13 @@
-/* eakv_oracle_avx512.c — the reference's CPU fused attention as it runs on
- * AVX-512 (kernels/fused_attention.ea:190-373, compiled by the Ea compiler to
- * 16-lane AVX-512), restated with intrinsics.
+/* eakv_oracle_avx512.c — the reference's CPU kernels as they run on AVX-512
+ * (compiled by the Ea compiler to 16 lanes), restated with intrinsics: the
+ * fused attention (kernels/fused_attention.ea:190-373), the K-score
+ * (fused_k_score*.ea) and the V-sum (fused_v_sum*.ea, fused_k_score_gqa*.ea).
  *
  * TEST INFRASTRUCTURE ONLY (see eakv_oracle.h): bench.py's CPU baseline times
- * it, and a test checks it against orc_fused_attention.  Per lane it does the
- * arithmetic of orc_fused_attention (the dequant fma, the 16-lane fma chain
- * over chunks, the halving reduction, expf, the V fma chain), so the two
- * agree bit for bit.  The functions carry their own target attribute: the
+ * them, and tests check them against the scalar oracle.  Per lane they do the
+ * oracle's arithmetic (the dequant fma, the 16-lane fma chain over chunks,
+ * the halving reduction, expf, the V fma chain over the tokens), so they
+ * agree with it bit for bit.  The functions carry their own target attribute: the
  * library loads on any x86-64 CPU and orc_avx512_available() says whether
  * they may be called.
  */
@@ -110,4 +111,80 @@ void orc_attention_fused_avx512(const orc_cache_t *c, const float *queries, int 
                                orc_cache_weights(c, layer, 1), orc_cache_scales(c, layer, 1),
                                orc_cache_biases(c, layer, 1), output_out, orc_cache_seq_len(c),
                                n_q_heads, n_kv_heads, gph);
+}
+
+/* The reference's unfused K-score on AVX-512 (fused_k_score.ea:161-235 and
+ * fused_k_score_gqa.ea:7-99, compiled to 16 lanes): per kv head and token
+ * the chunks are dequantized once (the GQA loop flip), then per q head one
+ * 16-lane fma chain over the chunks, the halving reduction and x rsqrt(d),
+ * which is orc_k_score_gqa's arithmetic, so the scores agree bit for bit. */
+AVX512 void orc_attention_scores_avx512(const orc_cache_t *c, const float *queries, int layer,
+                                        int n_q_heads, int n_kv_heads, float *scores_out)
+{
+    const int hd = orc_cache_head_dim(c), L = orc_cache_seq_len(c);
+    const int gpd = hd / 64, n_chunks = hd / 16, qpk = n_q_heads / n_kv_heads;
+    const int64_t gph = (int64_t)orc_cache_max_seq_len(c) * gpd;
+    const uint8_t *kw = orc_cache_weights(c, layer, 0);
+    const float *ks = orc_cache_scales(c, layer, 0), *kb = orc_cache_biases(c, layer, 0);
+    volatile float dv = (float)hd;
+    const float rs = 1.0f / sqrtf(dv);
+    for (int kvh = 0; kvh < n_kv_heads; kvh++) {
+        const int64_t goff = (int64_t)kvh * gph;
+        for (int t = 0; t < L; t++) {
+            const int64_t g0 = goff + (int64_t)t * gpd;
+            __m512 k[8];
+            for (int ch = 0; ch < n_chunks; ch++) {
+                const int64_t g = g0 + ch / 4;
+                k[ch] = deq16(kw + g * 32, ch & 3, _mm512_set1_ps(ks[g]), _mm512_set1_ps(kb[g]));
+            }
+            for (int o = 0; o < qpk; o++) {
+                const int qh = kvh * qpk + o;
+                const float *qv = queries + (int64_t)qh * hd;
+                __m512 acc = _mm512_setzero_ps();
+                for (int ch = 0; ch < n_chunks; ch++)
+                    acc = _mm512_fmadd_ps(k[ch], _mm512_loadu_ps(qv + 16 * ch), acc);
+                scores_out[(int64_t)qh * L + t] = reduce16(acc) * rs;
+            }
+        }
+    }
+}
+
+/* The reference's unfused V-sum on AVX-512 (fused_v_sum.ea:83-163,
+ * fused_v_sum_64.ea:55-110; GQA fused_k_score_gqa.ea:106-305, which takes
+ * the q heads of a kv head in pairs and dequantizes V once per token and
+ * pair): every output element is one fma chain over the tokens in order,
+ * orc_v_sum_gqa's arithmetic, so the outputs agree bit for bit. */
+AVX512 void orc_attention_output_avx512(const orc_cache_t *c, const float *weights, int layer,
+                                        int n_q_heads, int n_kv_heads, float *output_out)
+{
+    const int hd = orc_cache_head_dim(c), L = orc_cache_seq_len(c);
+    const int gpd = hd / 64, n_chunks = hd / 16, qpk = n_q_heads / n_kv_heads;
+    const int64_t gph = (int64_t)orc_cache_max_seq_len(c) * gpd;
+    const uint8_t *vw = orc_cache_weights(c, layer, 1);
+    const float *vs = orc_cache_scales(c, layer, 1), *vb = orc_cache_biases(c, layer, 1);
+    for (int kvh = 0; kvh < n_kv_heads; kvh++) {
+        const int64_t goff = (int64_t)kvh * gph;
+        for (int o0 = 0; o0 < qpk; o0 += 2) {
+            const int np = qpk - o0 < 2 ? 1 : 2;
+            const int qh0 = kvh * qpk + o0;
+            __m512 acc[2][8];
+            for (int p = 0; p < 2; p++)
+                for (int ch = 0; ch < 8; ch++) acc[p][ch] = _mm512_setzero_ps();
+            for (int t = 0; t < L; t++) {
+                const int64_t g0 = goff + (int64_t)t * gpd;
+                const __m512 w0 = _mm512_set1_ps(weights[(int64_t)qh0 * L + t]);
+                const __m512 w1 = _mm512_set1_ps(np > 1 ? weights[(int64_t)(qh0 + 1) * L + t] : 0.0f);
+                for (int ch = 0; ch < n_chunks; ch++) {
+                    const int64_t g = g0 + ch / 4;
+                    const __m512 v = deq16(vw + g * 32, ch & 3, _mm512_set1_ps(vs[g]),
+                                           _mm512_set1_ps(vb[g]));
+                    acc[0][ch] = _mm512_fmadd_ps(v, w0, acc[0][ch]);
+                    acc[1][ch] = _mm512_fmadd_ps(v, w1, acc[1][ch]);
+                }
+            }
+            for (int p = 0; p < np; p++)
+                for (int ch = 0; ch < n_chunks; ch++)
+                    _mm512_storeu_ps(output_out + (int64_t)(qh0 + p) * hd + 16 * ch, acc[p][ch]);
+        }
+    }
 }

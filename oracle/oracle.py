@@ -50,6 +50,8 @@ _SIG = {
     "orc_attention_output": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "orc_attention_fused": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "orc_attention_fused_avx512": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "orc_attention_scores_avx512": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "orc_attention_output_avx512": (None, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "orc_avx512_available": (C.c_int, []),
     "orc_cache_seq_len": (C.c_int, [_vp]),
     "orc_cache_n_layers": (C.c_int, [_vp]),
@@ -297,6 +299,24 @@ class OracleCache:
         q = _f32(q)
         out = np.zeros((n_q, self.head_dim), np.float32)
         lib().orc_attention_fused(self.h, _p(q), layer, n_q, n_kv, _p(out))
+        return out
+
+    def attention_scores_avx512(self, q, layer, n_q, n_kv):
+        """attention_scores on AVX-512 (bit-identical); needs avx512_available()."""
+        if not avx512_available():
+            raise RuntimeError("this CPU lacks AVX-512 (F, BW, DQ, VL)")
+        q = _f32(q)
+        out = np.zeros((n_q, self.seq_len), np.float32)
+        lib().orc_attention_scores_avx512(self.h, _p(q), layer, n_q, n_kv, _p(out))
+        return out
+
+    def attention_output_avx512(self, w, layer, n_q, n_kv):
+        """attention_output on AVX-512 (bit-identical); needs avx512_available()."""
+        if not avx512_available():
+            raise RuntimeError("this CPU lacks AVX-512 (F, BW, DQ, VL)")
+        w = _f32(w)
+        out = np.zeros((n_q, self.head_dim), np.float32)
+        lib().orc_attention_output_avx512(self.h, _p(w), layer, n_q, n_kv, _p(out))
         return out
 
     def attention_fused_avx512(self, q, layer, n_q, n_kv):

@@ -230,9 +230,8 @@ def test_v_sum_signed_and_nonfinite_weights(E, rng, nh, n_q, n_kv, d, L, lmax):
 def test_large_groups_fused_and_v_sum(E, rng, nh, n_q, n_kv, d, L, lmax):
     """More than 8 q heads per kv head (MQA and wide GQA): the matrix-core
     programs split the group into virtual kv heads of at most 8 q heads that
-    read the same kv head (16 -> 2 x 8, 24 -> 3 x 8, 10 -> 2 x 5, 12 -> 2 x 6);
-    11 has no such split and runs the VALU programs.  Fused attention and
-    the V-sum against the oracle."""
+    read the same kv head (16 -> 2 x 8, 24 -> 3 x 8, 10 -> 2 x 5, 12 -> 2 x 6,
+    11 -> 11 x 1).  Fused attention and the V-sum against the oracle."""
     say("large-groups", nh, n_q, n_kv, d, L)
     g, o = loaded(E, rng, nh, d, L, lmax)
     q = (rng.standard_normal((n_q, d)) * 2).astype(np.float32)

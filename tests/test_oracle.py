@@ -263,6 +263,30 @@ def test_avx512_fused_attention_is_the_scalar_one(rng, d, n_q, n_kv, L):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+@pytest.mark.skipif(not O.avx512_available(), reason="this CPU lacks AVX-512")
+@pytest.mark.parametrize("d,n_q,n_kv,L", [(128, 8, 8, 300), (64, 4, 4, 77), (128, 32, 8, 129),
+                                          (64, 32, 4, 64), (128, 7, 1, 33), (128, 3, 3, 0)])
+def test_avx512_unfused_kernels_are_the_scalar_ones(rng, d, n_q, n_kv, L):
+    """The CPU baseline's AVX-512 K-score and V-sum (16-lane intrinsics, the
+    GQA loop flip, q heads in pairs, an odd head alone) against the scalar
+    restatement: equal bit for bit, with signed and non-finite weights."""
+    c = O.OracleCache(2, n_kv, d, max(L, 1) + 5)
+    if L:
+        c.load_raw((rng.standard_normal((2, 2, n_kv, L, d)) * 2).astype(np.float32), L)
+    q = (rng.standard_normal((n_q, d)) * 1.5).astype(np.float32)
+    for layer in (0, 1):
+        a = c.attention_scores(q, layer, n_q, n_kv)
+        b = c.attention_scores_avx512(q, layer, n_q, n_kv)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        w = rng.standard_normal((n_q, L)).astype(np.float32)
+        if L > 3:
+            w[0, 3] = np.nan
+            w[-1, 1] = np.inf
+        a = c.attention_output(w, layer, n_q, n_kv)
+        b = c.attention_output_avx512(w, layer, n_q, n_kv)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 # ------------------------------------------------- dequantize range, validate
 
 def test_dequantize_range_is_a_slice_of_the_closed_form(rng):
