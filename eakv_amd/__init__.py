@@ -70,6 +70,8 @@ SIGNATURES = {
     "eakv_attention_fused": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "eakv_attention_fused_batch_device": (
         C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "eakv_attention_fused_batch_device_noalloc": (
+        C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp]),
     "eakv_dequantize_range_device": (
         C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp, _vp]),
     "eakv_dequantize_range": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp]),

@@ -245,3 +245,60 @@ int eakv_attention_fused(const eakv_cache_t *cc, const float *queries,
     eakvi_leave(prev);
     return rc;
 }
+
+/* The batched fused call with its chunk partials in the library's static
+ * device scratch (eakvd_scratch) instead of caches[0]'s workspace: no
+ * allocation on any path.  Calls on one device share that scratch, so calls
+ * that overlap in time on one device race; their ordering is the caller's. */
+int eakv_attention_fused_batch_device_noalloc(eakv_cache_t *const *caches,
+                                              int n_caches, int layer,
+                                              const float *d_q, int n_q, int n_kv,
+                                              float *d_out, void *stream)
+{
+    if (!caches || n_caches <= 0 || n_caches > EAKVD_MAX_BATCH || !d_q || !d_out)
+        return eakvi_set_error(EAKV_ERR_INVALID, "fused_noalloc: invalid argument");
+    for (int i = 0; i < n_caches; i++) {
+        if (!caches[i])
+            return eakvi_set_error(EAKV_ERR_INVALID, "fused_noalloc: NULL cache");
+        const eakv_cache_t *a = caches[0], *b = caches[i];
+        if (a->n_layers != b->n_layers || a->n_kv_heads != b->n_kv_heads ||
+            a->head_dim != b->head_dim || a->max_seq_len != b->max_seq_len ||
+            a->device != b->device)
+            return eakvi_set_error(EAKV_ERR_INVALID,
+                                  "fused_noalloc: caches differ in shape");
+    }
+    eakv_cache_t *c0 = caches[0];
+    int rc = attn_check(c0, layer, n_q, n_kv);
+    if (rc) return rc;
+    eakvd_batch b;
+    memset(&b, 0, sizeof(b));
+    b.n_seq = n_caches;
+    for (int i = 0; i < n_caches; i++) {
+        b.base[i] = caches[i]->dev;
+        b.seq_len[i] = caches[i]->seq_len;
+    }
+    const size_t need = eakvd_fused_launch_bytes(&c0->geom, &b, n_q, n_kv);
+    if (need > EAKVD_SCRATCH_BYTES)
+        return eakvi_set_error(EAKV_ERR_INVALID,
+                              "fused_noalloc: %zu bytes of partials needed, the static "
+                              "scratch holds %zu", need, (size_t)EAKVD_SCRATCH_BYTES);
+    int prev;
+    rc = eakvi_enter(c0, &prev);
+    if (rc) return rc;
+    void *st = eakvi_stream_or_default(c0, stream);
+    /* the caches' own streams: device-side waits with their events, which
+     * exist from creation on */
+    for (int i = 0; rc == EAKV_OK && i < n_caches; i++)
+        rc = eakvi_order_before(caches[i], st);
+    void *scr = NULL;
+    if (rc == EAKV_OK) {
+        int e = eakvd_scratch(&scr);
+        if (e) rc = eakvi_hip_fail(e, "fused_noalloc: scratch address");
+    }
+    if (rc == EAKV_OK) {
+        int e = eakvd_fused(&c0->geom, &b, layer, d_q, n_q, n_kv, d_out, scr, st);
+        if (e) rc = eakvi_hip_fail(e, "fused_noalloc launch");
+    }
+    eakvi_leave(prev);
+    return rc;
+}

@@ -126,6 +126,13 @@ int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
 size_t eakvd_fused_launch_bytes(const eakvd_geom *g, const eakvd_batch *b,
                                 int n_q, int n_kv);
 
+/* The library's static device scratch for the allocation-free entry point
+ * (hip/fused.hip): EAKVD_SCRATCH_BYTES per device, held until the process
+ * ends.  *p = its address on the current device (looked up once per device).
+ * Returns 0 or a HIP error. */
+#define EAKVD_SCRATCH_BYTES ((size_t)16 << 20)
+int eakvd_scratch(void **p);
+
 /* ---- whole-plane kernels (hip/planes.hip)
  * eakvd_dequantize: groups [g0, g0 + n) of block (layer, kv) to out
  * (f32[n][64], device).  eakvd_validate: the integrity check of the first n

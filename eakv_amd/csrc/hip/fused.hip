@@ -39,9 +39,15 @@
 //   with the reference arithmetic, then V by dims; same partial/merge scheme.
 #include <string.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
+
+// Static device scratch of the allocation-free entry point: the chunk
+// partials of one launch.  Host code never uses this name as an address: it
+// takes the device address from hipGetSymbolAddress (eakvd_scratch).
+static __device__ __align__(256) uint8_t scratch[EAKVD_SCRATCH_BYTES];
 
 namespace {
 
@@ -1443,6 +1449,26 @@ extern "C" size_t eakvd_fused_launch_bytes(const eakvd_geom *g, const eakvd_batc
     // partial (m, l, o[D]) of every (sequence, q head, chunk)
     const FusedPlan p = fused_plan(g, b, n_q, n_kv);
     return (size_t)b->n_seq * n_q * p.mc * (g->head_dim + 2) * sizeof(float);
+}
+
+extern "C" int eakvd_scratch(void **p)
+{
+    // one lookup per device: each device holds its own copy of `scratch`
+    static std::mutex mu;
+    static void *addr[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void *a = nullptr;
+        e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        addr[dev] = a;
+    }
+    *p = addr[dev];
+    return 0;
 }
 
 extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,

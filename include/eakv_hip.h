@@ -99,6 +99,23 @@ int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
                                       int n_kv_heads, float *d_out,
                                       void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): eakv_attention_fused_batch_device with the chunk
+ * partials in the library's static device scratch of 16 MiB per device
+ * instead of caches[0]'s workspace, so no call path allocates.  Same
+ * arguments, results and stream ordering; EAKV_ERR_INVALID when the launch
+ * would need more than 16 MiB of partials (n_caches * n_q_heads * chunks *
+ * (head_dim + 2) * 4 bytes: 1.1 MB for 8 caches of 32 q heads over 32K
+ * tokens, 1.1 MB for 64 q heads over 128K tokens).
+ * Every call on one device shares that scratch: calls that overlap in time
+ * on one device race, and ordering them is the caller's. */
+int eakv_attention_fused_batch_device_noalloc(eakv_cache_t *const *caches,
+                                              int n_caches, int layer,
+                                              const float *d_q, int n_q_heads,
+                                              int n_kv_heads, float *d_out,
+                                              void *stream);
+
 /* Dequantize groups [group_start, group_start + group_count) of the (layer,
  * kv_idx) planes to f32, 64 values per group in group order: value =
  * fma(nibble, scale, bias) with byte k of a group holding dim k (low nibble)
