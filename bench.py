@@ -1,20 +1,32 @@
-"""Benchmark: fused Q4 decode attention on one MI355X.
+"""Benchmark: fused Q4 decode attention on one MI355X, every workload.
 
-Default workload (Llama-3-8B-shape GQA, the headline metric): 8 independent
-caches (8 concurrent sequences), 32 layers, 32 q heads / 8 kv heads, d=128,
-32K context.  One step = append one new token to every sequence (all layers,
-K and V, one batched quantize launch), then fused attention over the full
+Headline (`value`): the Llama-3-8B-shape GQA workload.  8 independent caches
+(8 concurrent sequences), 32 layers, 32 q heads / 8 kv heads, d=128, 32K
+context.  One step = append one new token to every sequence (all layers, K
+and V, one batched quantize launch), then fused attention over the full
 32768-token context for every layer (one launch per layer covering all 8
 sequences), then O(1) restore to 32767 tokens so every step sees the same
 context.  Inputs are synthetic, seeded, generated on the device; the caches
 and queries are resident in HBM before the timed region starts.
 
-Prints ONE JSON line.  `value` is the whole step time per layer (µs);
-`roofline` is the fused attention launch: algorithmic bytes (K and V Q4 read
-once: 160 B per token-head at d=128, plus q in and out) over its average
-duration from HIP events on its stream.  `cpu_baseline` is the CPU oracle's
-two-pass fused attention (oracle/eakv_oracle.c) on a bounded sample of the
-same workload, run on this host's cores.
+`configs` holds every workload, each with its own timed steps and its CPU
+baseline from the same run:
+  1  8Q/8KV d128, 2048 tokens, 1 layer: the unfused API step
+     (eakv_attention_scores -> row softmax -> eakv_attention_output);
+  2  32Q/4KV d64, 4096 tokens, 22 layers: the same per layer;
+  3  32Q/32KV d128, 8192 tokens, 32 layers: the same per layer;
+  4  the headline workload above;
+  5  64Q/8KV d128, 80 layers: bulk quantization of the full 131072-token
+     cache, then 64 decode steps of (append one token to every layer, fused
+     attention over every layer), the context growing to 131136.
+Configs 1-3 also report the fused call on the same caches.
+
+Prints ONE JSON line.  `roofline` is the headline's fused attention launch:
+algorithmic bytes (K and V Q4 read once: 160 B per token-head at d=128, plus
+q in and out) over its mean duration from HIP events on its stream.
+`cpu_baseline` is the reference's CPU kernels restated with AVX-512
+intrinsics (the oracle, bit-identical to its scalar form) on a bounded
+sample of the same workload, on this host's cores.
 """
 from __future__ import annotations
 
@@ -33,20 +45,34 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 SEED_BASE = 0xEA4B
+# worker threads for the all-core CPU baseline: every CPU this process may
+# run on, at most the 16-CPU share of one GPU on the benchmark hosts
+CPU_THREADS_MAX = 16
 
-# name, layers, q heads, kv heads, d, context, sequences, K dist, V dist
+# name, layers, q heads, kv heads, d, context, sequences, K dist, V dist,
+# path: "unfused" (scores -> softmax -> output), "fused" (append + fused,
+# context restored each step) or "grow" (append + fused, context growing)
 CONFIGS = {
     1: dict(name="mha-8h-d128-2k", nl=1, nq=8, nkv=8, d=128, L=2048, nseq=1,
-            k="normal", v="normal"),
+            k="normal", v="normal", path="unfused"),
     2: dict(name="tinyllama-gqa8-d64-4k", nl=22, nq=32, nkv=4, d=64, L=4096, nseq=1,
-            k="chan", v="normal"),
+            k="chan", v="normal", path="unfused"),
     3: dict(name="llama2-7b-mha-d128-8k", nl=32, nq=32, nkv=32, d=128, L=8192, nseq=1,
-            k="drift", v="drift"),
+            k="drift", v="drift", path="unfused"),
     4: dict(name="llama3-8b-gqa4-d128-32k-x8", nl=32, nq=32, nkv=8, d=128, L=32768,
-            nseq=8, k="chan", v="normal"),
+            nseq=8, k="chan", v="normal", path="fused"),
     5: dict(name="70b-gqa8-d128-128k", nl=80, nq=64, nkv=8, d=128, L=131072, nseq=1,
-            k="chan_outlier", v="chan_outlier"),
+            k="chan_outlier", v="chan_outlier", path="grow"),
 }
+HEADLINE = 4
+DTYPE = ("q4_1 planes (u8 nibbles, f32 scale and bias per 64 values); fused and V-sum dots "
+         "on int8 matrix cores (q and softmax weights as 32-bit fixed point in balanced int8 "
+         "digits, exact int32 sums), f32 softmax and recombination; unfused K-score f32 fma")
+
+
+def metric_text(c):
+    return (f"fused Q4 attn µs/layer + achieved HBM GB/s, {c['nq']}Q/{c['nkv']}KV "
+            f"d{c['d']} {c['L'] // 1024}K ctx, 1 GPU")
 
 
 class Synth:
@@ -63,6 +89,9 @@ class Synth:
         self.lib.eakv_synth_fill.restype = C.c_int
         self.lib.eakv_synth_fill.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int,
                                              C.POINTER(self.Params), C.c_void_p]
+        self.lib.eakv_synth_softmax.restype = C.c_int
+        self.lib.eakv_synth_softmax.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                                C.c_void_p]
 
     def fill(self, ptr, n_rows, n_tok, d, seed, row0, pos0, kind, chan_ptr=None,
              stream=None):
@@ -77,6 +106,11 @@ class Synth:
         rc = self.lib.eakv_synth_fill(ptr, n_rows, n_tok, d, C.byref(p), stream)
         if rc:
             raise RuntimeError(f"synth launch failed: {rc}")
+
+    def softmax(self, scores, w, n_rows, L, stream=None):
+        rc = self.lib.eakv_synth_softmax(scores, w, n_rows, L, stream)
+        if rc:
+            raise RuntimeError(f"softmax launch failed: {rc}")
 
 
 def channel_scales(cfg, seed):
@@ -97,6 +131,12 @@ def channel_scales(cfg, seed):
 
 
 class Workload:
+    """The caches of one configuration, filled on the device, and its step.
+
+    fused: the caches hold L-1 tokens; a step appends token L-1 and restores
+    afterwards.  grow: the caches hold L tokens and each step appends the
+    next one (max_seq_len L + 64).  unfused: the caches hold L tokens."""
+
     def __init__(self, cfg_id, ctx=None):
         import eakv_amd as E
         from eakv_amd import hipmem as H
@@ -106,7 +146,9 @@ class Workload:
             self.cfg["L"] = ctx
         c = self.cfg
         self.seed = SEED_BASE + cfg_id
-        self.L0 = c["L"] - 1                     # each step appends token L-1
+        self.grow = c["path"] == "grow"
+        # the unfused step reads the cache as filled; the decode steps append
+        self.L0 = c["L"] if c["path"] in ("grow", "unfused") else c["L"] - 1
         self.lmax = c["L"] + 64
         self.synth = Synth()
         self.caches = [E.Cache(c["nl"], c["nkv"], c["d"], self.lmax) for _ in range(c["nseq"])]
@@ -117,11 +159,19 @@ class Workload:
         self.tok = H.DeviceArray((c["nseq"], c["nl"], 2, c["nkv"], 1, c["d"]))
         self.quant_ms = None
 
+    def free(self):
+        for c in self.caches:
+            c.free()
+        for a in (self.chan, self.out, self.tok):
+            a.free()
+        for a in getattr(self, "ql", []):
+            a.free()
+
     def row0(self, s, layer, kv):
         c = self.cfg
         return ((s * c["nl"] + layer) * 2 + kv) * c["nkv"]
 
-    def fill_context(self, time_quantize=True):
+    def fill_context(self):
         """Synthesize and quantize L0 tokens per layer of every sequence; the
         quantize launches are timed with events."""
         E, H, c = self.E, self.H, self.cfg
@@ -150,28 +200,6 @@ class Workload:
         self.quant_ms = qtime
         self.quant_bytes = (c["nseq"] * c["nl"] * 2 * c["nkv"] * self.L0 * c["d"]) * (4 + 0.625)
 
-    def step(self, events=None):
-        """Append the token at position L0 everywhere, attend every layer,
-        rewind to L0.  events: a pair recorded on the launch stream right
-        before the first and right after the last fused-attention call (no
-        event between the calls: each is a barrier that drains the queue)."""
-        E, c = self.E, self.cfg
-        rc = E.lib().eakv_append_batch_device(self.handles, c["nseq"], self.tok.ptr, 1, None)
-        assert rc == 0, E.last_error()
-        for cache in self.caches:
-            cache.advance(1)
-        if events:
-            events[0].record(self.stream)
-        for l in range(c["nl"]):
-            rc = E.lib().eakv_attention_fused_batch_device(
-                self.handles, c["nseq"], l, self.ql[l].ptr, c["nq"], c["nkv"],
-                self.out.ptr, None)
-            assert rc == 0, E.last_error()
-        if events:
-            events[1].record(self.stream)
-        for cache in self.caches:
-            cache.restore(self.L0)
-
     def prepare_step_inputs(self):
         """New-token K/V in the batched-append layout
         [seq][layer][kv][head][1][d] and per-layer queries [seq][q][d]."""
@@ -191,86 +219,270 @@ class Workload:
                             (l + 1) << 20, 0, "normal", stream=self.stream)
             self.ql.append(a)
 
-    def fused_bytes(self):
+    def step(self, events=None):
+        """Append the next token everywhere, attend every layer (and, for
+        the restored context, rewind to L0).  events: a pair recorded on the
+        launch stream right before the first and right after the last
+        fused-attention call (no event between the calls: each is a barrier
+        that drains the queue)."""
+        E, c = self.E, self.cfg
+        rc = E.lib().eakv_append_batch_device(self.handles, c["nseq"], self.tok.ptr, 1, None)
+        assert rc == 0, E.last_error()
+        for cache in self.caches:
+            cache.advance(1)
+        if events:
+            events[0].record(self.stream)
+        for l in range(c["nl"]):
+            rc = E.lib().eakv_attention_fused_batch_device(
+                self.handles, c["nseq"], l, self.ql[l].ptr, c["nq"], c["nkv"],
+                self.out.ptr, None)
+            assert rc == 0, E.last_error()
+        if events:
+            events[1].record(self.stream)
+        if not self.grow:
+            for cache in self.caches:
+                cache.restore(self.L0)
+
+    def fused_bytes(self, ctx=None):
         c = self.cfg
-        ctx = self.L0 + 1
+        ctx = ctx if ctx is not None else self.L0 + 1
         per_token_head = 2 * (c["d"] // 64) * 40
         return c["nseq"] * (c["nkv"] * ctx * per_token_head + c["nq"] * c["d"] * 4 * 2)
 
+    def unfused_bytes(self):
+        """K-score: K planes + scores written + q; softmax: scores read,
+        weights written; V-sum: V planes + weights read + out."""
+        c = self.cfg
+        L, planes = self.L0, c["nkv"] * self.L0 * (c["d"] // 64) * 40
+        ks = planes + c["nq"] * L * 4 + c["nq"] * c["d"] * 4
+        sm = 2 * c["nq"] * L * 4
+        vs = planes + c["nq"] * L * 4 + c["nq"] * c["d"] * 4
+        return ks, sm, vs
 
-def cpu_baseline(cfg, budget_s=12.0):
-    """Time the reference's CPU fused attention (the oracle's two-pass
-    restatement of fused_attention.ea, on AVX-512 where the host has it, as
-    the reference's kernels compile; else the scalar restatement) over one
-    sequence x one layer, all q heads, full context: the median of up to 50
-    single-threaded runs after a warmup, then up to 24 units per thread spread
-    over up to 16 threads (10-20 s of CPU work at the 32K configuration).
-    Per layer = per unit x the configuration's sequences."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
-    nkv, nq, d, L = cfg["nkv"], cfg["nq"], cfg["d"], cfg["L"]
-    rng = np.random.default_rng(SEED_BASE)
-    oc = O.OracleCache(1, nkv, d, L)
-    data = rng.standard_normal((1, 2, nkv, L, d), dtype=np.float32)
-    oc.load_raw(data, L)
-    del data
-    q = rng.standard_normal((nq, d)).astype(np.float32)
-    avx = O.avx512_available()
-    run = (lambda: oc.attention_fused_avx512(q, 0, nq, nkv)) if avx else \
-        (lambda: oc.attention_fused(q, 0, nq, nkv))
+
+def timed(H, stream, fn, steps, warmup, per):
+    """Mean µs per unit of `fn` (one call = `per` units) between two events
+    on `stream`, after `warmup` untimed calls."""
+    for _ in range(warmup):
+        fn()
+    H.synchronize()
+    e0, e1 = H.Event(), H.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) * 1e3 / (steps * per)
+
+
+# ---------------------------------------------------------------- CPU side
+
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count() or 1
+    return {"cpu_model": model, "host_cpus": os.cpu_count(), "affinity_cpus": aff,
+            "threads": max(1, min(CPU_THREADS_MAX, aff))}
+
+
+def cpu_time(run, budget_s):
+    """The reference benchmark's method (bench_libeakv.c:17-39): a warmup,
+    then the median of up to 50 single-threaded runs; then the same unit on
+    every worker thread at once, three rounds, each unit's time = round time
+    / units.  Returns (single s, [all-core s per unit per round], threads,
+    single runs, units per round)."""
+    info = cpu_info()
     t0 = time.perf_counter()
-    run()                                                   # warmup
+    run()
     first = time.perf_counter() - t0
-    n1 = int(max(3, min(50, budget_s / 2 / max(first, 1e-4))))
+    n1 = int(max(5, min(50, budget_s / 2 / max(first, 1e-5))))
     times = []
     for _ in range(n1):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
     single = float(np.median(times))
-    threads = max(1, min(16, os.cpu_count() or 1))
-    reps = threads * max(1, min(24, int(budget_s / 2 / max(single, 1e-4) / 2)))
-    t0 = time.perf_counter()
+    threads = info["threads"]
+    per_thread = max(1, min(8, int(budget_s / 6 / max(single, 1e-5))))
+    units = threads * per_thread
+    rounds = []
     with ThreadPoolExecutor(threads) as ex:
-        list(ex.map(lambda _: run(), range(reps)))
-    allcore = (time.perf_counter() - t0) / reps             # s per unit, all threads busy
-    per_layer_us = lambda unit_s: unit_s * cfg["nseq"] * 1e6
-    what = ("AVX-512 restatement (16-lane intrinsics, bit-identical to the scalar oracle)"
-            if avx else "scalar C restatement (this host lacks AVX-512)")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            list(ex.map(lambda _: run(), range(units)))
+            rounds.append((time.perf_counter() - t0) / units)
+    return single, rounds, threads, n1, units
+
+
+def cpu_baseline(cfg, budget_s=6.0):
+    """The reference's CPU path for one (sequence, layer) unit of the
+    workload on this host, scaled to one layer-step (x sequences):
+    fused workloads the two-pass fused attention (fused_attention.ea,
+    extended to GQA), unfused ones K-score -> softmax -> V-sum
+    (fused_k_score*.ea, fused_v_sum*.ea, fused_k_score_gqa*.ea), on AVX-512
+    where the host has it (the oracle's intrinsics restatement, bit-identical
+    to its scalar form), else the scalar restatement.  Inputs: N(0,1) (the
+    timing does not depend on the values); the full context of the workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    nkv, nq, d, L = cfg["nkv"], cfg["nq"], cfg["d"], cfg["L"]
+    rng = np.random.default_rng(SEED_BASE)
+    oc = O.OracleCache(1, nkv, d, L)
+    block = rng.standard_normal(1 << 22, dtype=np.float32)
+    oc.load_raw(np.resize(block, 2 * nkv * L * d), L)
+    q = rng.standard_normal((nq, d)).astype(np.float32)
+    avx = O.avx512_available()
+    if cfg["path"] == "unfused":
+        sc = (oc.attention_scores_avx512 if avx else oc.attention_scores)
+        out = (oc.attention_output_avx512 if avx else oc.attention_output)
+        what = "K-score -> row softmax -> V-sum"
+
+        def run():
+            out(O.softmax_rows(sc(q, 0, nq, nkv)), 0, nq, nkv)
+    else:
+        fused = oc.attention_fused_avx512 if avx else oc.attention_fused
+        what = "two-pass fused attention"
+
+        def run():
+            fused(q, 0, nq, nkv)
+    single, rounds, threads, n1, units = cpu_time(run, budget_s)
+    oc.free()
+    scale = cfg["nseq"] * 1e6
+    info = cpu_info()
+    isa = ("AVX-512 restatement (16-lane intrinsics, bit-identical to the scalar oracle)"
+           if avx else "scalar C restatement (this host lacks AVX-512)")
     return {
-        "value": round(per_layer_us(allcore), 1), "unit": "us/layer",
+        "value": round(float(np.median(rounds)) * scale, 1), "unit": "us/layer",
         "cores": threads, "kind": "port", "isa": "avx512" if avx else "scalar",
-        "single_core_us_per_layer": round(per_layer_us(single), 1),
-        "sample": (f"reference CPU fused attention (fused_attention.ea two-pass, extended "
-                   f"to GQA), {what}: 1 sequence x 1 layer, {nq}q/{nkv}kv d{d} ctx {L}; "
-                   f"single-threaded median of {n1} runs after a warmup; {reps} runs on "
-                   f"{threads} threads; scaled x{cfg['nseq']} sequences per layer"),
+        "single_core_us_per_layer": round(single * scale, 1),
+        "all_core_us_per_layer_rounds": [round(r * scale, 1) for r in rounds],
+        "host_cpus": info["host_cpus"], "affinity_cpus": info["affinity_cpus"],
+        "cpu_model": info["cpu_model"],
+        "sample": (f"reference CPU {what}, {isa}: 1 sequence x 1 layer, {nq}q/{nkv}kv d{d} "
+                   f"ctx {L}; single-threaded median of {n1} runs after a warmup; 3 rounds of "
+                   f"{units} units on {threads} threads (all-core value = median round); "
+                   f"x{cfg['nseq']} sequences per layer-step"),
     }
 
 
-def copy_calibration(n_bytes, reps=5):
-    """Copy n_bytes device-to-device `reps` times with the synth library's
-    streaming copy kernel; prints the bytes read and written per launch."""
-    from eakv_amd import hipmem as H
-    lib = Synth().lib
-    lib.eakv_synth_copy.restype = C.c_int
-    lib.eakv_synth_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
-    src = H.DeviceArray((n_bytes // 4,))
-    dst = H.DeviceArray((n_bytes // 4,))
-    e0, e1 = H.Event(), H.Event()
-    ms = []
-    for _ in range(reps):
-        e0.record(None)
-        rc = lib.eakv_synth_copy(dst.ptr, src.ptr, n_bytes, None)
-        if rc:
-            raise RuntimeError(f"copy launch failed: {rc}")
-        e1.record(None)
-        e1.synchronize()
-        ms.append(e0.elapsed_ms(e1))
-    print(json.dumps({"copy_bytes_read": n_bytes, "copy_bytes_written": n_bytes,
-                      "launches": reps, "ms": [round(m, 4) for m in ms],
-                      "gbs_read_plus_write": round(2 * n_bytes / min(ms) / 1e6, 1)}),
-          flush=True)
+def cpu_quantize_baseline(cfg, budget_s=4.0):
+    """The reference's bulk quantization (quantize_simd.ea, scalar; the
+    oracle's restatement) on a 64 MiB sample of the workload's f32 KV:
+    GB/s of algorithmic bytes (4 B read + 0.625 B written per value)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    nkv, d = cfg["nkv"], cfg["d"]
+    L = (64 << 20) // (2 * nkv * d * 4)
+    data = np.resize(np.random.default_rng(SEED_BASE).standard_normal(1 << 22, dtype=np.float32),
+                     2 * nkv * L * d)
+    caches = {}
+
+    def run():
+        import threading
+        k = threading.get_ident()
+        if k not in caches:
+            caches[k] = O.OracleCache(1, nkv, d, L)
+        caches[k].load_raw(data, L)
+    single, rounds, threads, n1, units = cpu_time(run, budget_s)
+    for c in caches.values():
+        c.free()
+    alg = data.size * 4.625
+    return {"single_core_gbs": round(alg / single / 1e9, 3),
+            "all_core_gbs": round(alg / float(np.median(rounds)) / 1e9, 3),
+            "all_core_gbs_rounds": [round(alg / r / 1e9, 3) for r in rounds],
+            "cores": threads,
+            "sample": f"{data.size * 4 >> 20} MiB of f32 ({nkv} kv heads x {L} tokens x d{d}, K and V), "
+                      f"scalar restatement of quantize_simd.ea; median of {n1} runs, 3 rounds of "
+                      f"{units} on {threads} threads"}
+
+
+# ---------------------------------------------------------------- GPU side
+
+def measure_fused(w, steps, warmup):
+    """The decode step (append + fused attention over every layer): ms per
+    step from the host clock around `steps` back-to-back steps, the fused
+    calls' mean from one event pair per step on the launch stream.  A
+    growing context is rewound after the warmup steps."""
+    H, c = w.H, w.cfg
+    for _ in range(warmup):
+        w.step()
+    H.synchronize()
+    if w.grow:
+        for cache in w.caches:
+            cache.restore(w.L0)
+    events = [[H.Event(), H.Event()] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for k in range(steps):
+        w.step(events[k])
+    H.synchronize()
+    total_s = time.perf_counter() - t0
+    fused = np.array([e0.elapsed_ms(e1) / c["nl"] for e0, e1 in events]) * 1e3
+    return total_s / steps * 1e3, float(fused.mean()), [round(float(x), 3) for x in
+                                                          np.percentile(fused, [0, 50, 100])]
+
+
+def measure_unfused(w, steps, warmup):
+    """The reference API's unfused step on the first cache, every layer:
+    eakv_attention_scores_device, the caller's row softmax, then
+    eakv_attention_output_device.  Per-call means of each phase (all layers
+    back to back, one event pair) and of the whole step."""
+    E, H, c = w.E, w.H, w.cfg
+    cache = w.caches[0]
+    L, nq, nkv, d = w.L0, c["nq"], c["nkv"], c["d"]
+    scores = H.DeviceArray((nq, L))
+    wts = H.DeviceArray((nq, L))
+    out = H.DeviceArray((nq, d))
+    lib = E.lib()
+
+    def ks():
+        for l in range(c["nl"]):
+            assert lib.eakv_attention_scores_device(cache.h, w.ql[l].ptr, l, nq, nkv,
+                                                    scores.ptr, None) == 0, E.last_error()
+
+    def sm():
+        for _ in range(c["nl"]):
+            w.synth.softmax(scores.ptr, wts.ptr, nq, L, w.stream)
+
+    def vs():
+        for l in range(c["nl"]):
+            assert lib.eakv_attention_output_device(cache.h, wts.ptr, l, nq, nkv, out.ptr,
+                                                    None) == 0, E.last_error()
+
+    def whole():
+        for l in range(c["nl"]):
+            assert lib.eakv_attention_scores_device(cache.h, w.ql[l].ptr, l, nq, nkv,
+                                                    scores.ptr, None) == 0, E.last_error()
+            w.synth.softmax(scores.ptr, wts.ptr, nq, L, w.stream)
+            assert lib.eakv_attention_output_device(cache.h, wts.ptr, l, nq, nkv, out.ptr,
+                                                    None) == 0, E.last_error()
+
+    res = {name: timed(H, w.stream, fn, steps, warmup, c["nl"])
+           for name, fn in (("k_score", ks), ("softmax", sm), ("v_sum", vs), ("step", whole))}
+    for a in (scores, wts, out):
+        a.free()
+    return res
+
+
+def fused_call_us(w, steps, warmup):
+    """Mean µs of one fused call per layer on the caches as filled (the
+    fused alternative to the unfused step)."""
+    E, H, c = w.E, w.H, w.cfg
+
+    def run():
+        for l in range(c["nl"]):
+            assert E.lib().eakv_attention_fused_batch_device(
+                w.handles, c["nseq"], l, w.ql[l].ptr, c["nq"], c["nkv"], w.out.ptr,
+                None) == 0, E.last_error()
+    return timed(H, w.stream, run, steps, warmup, c["nl"])
 
 
 def read_peak(n_bytes, regions=8, reps=3):
@@ -306,6 +518,263 @@ def read_peak(n_bytes, regions=8, reps=3):
     return n_bytes / best / 1e6
 
 
+def gbs(nbytes, us):
+    return nbytes / (us * 1e-6) / 1e9
+
+
+def run_config(cid, steps, warmup, ctx=None, with_cpu=True, log=print):
+    """Fill, time and (optionally) CPU-baseline one configuration; returns
+    (summary dict, workload internals for the headline line)."""
+    H = __import__("eakv_amd.hipmem", fromlist=["x"])
+    w = Workload(cid, ctx)
+    c = w.cfg
+    log(f"bench: config {cid} {c['name']}: filling {c['nseq']} x {c['nl']} layers x "
+        f"{w.L0} tokens")
+    w.fill_context()
+    w.prepare_step_inputs()
+    H.synchronize()
+    qgbs = w.quant_bytes / w.quant_ms / 1e6
+    r = {"workload": c["name"], "layers": c["nl"], "q_heads": c["nq"], "kv_heads": c["nkv"],
+         "head_dim": c["d"], "context": w.L0 + (0 if c["path"] == "unfused" else 1),
+         "sequences": c["nseq"]}
+    extra = {}
+    if c["path"] == "unfused":
+        u = measure_unfused(w, max(steps, 10), warmup)
+        ks_b, sm_b, vs_b = w.unfused_bytes()
+        alg = ks_b + sm_b + vs_b
+        fz = fused_call_us(w, max(steps, 10), warmup)
+        r.update({
+            "path": "eakv_attention_scores_device -> row softmax -> eakv_attention_output_device",
+            "us_per_layer_step": round(u["step"], 3),
+            "gbs": round(gbs(alg, u["step"]), 1), "frac": round(gbs(alg, u["step"]) / HBM_PEAK_GBS, 4),
+            "alg_bytes_per_layer_step": alg,
+            "kernels_us_per_layer": {k: round(u[k], 3) for k in ("k_score", "softmax", "v_sum")},
+            "k_score_gbs": round(gbs(ks_b, u["k_score"]), 1),
+            "v_sum_gbs": round(gbs(vs_b, u["v_sum"]), 1),
+            "fused_call_us_per_layer": round(fz, 3),
+            "fused_call_gbs": round(gbs(w.fused_bytes(w.L0), fz), 1),
+        })
+        extra = {"ms_step": u["step"] * c["nl"] / 1e3, "fused_us": u["step"], "alg": alg,
+                 "steps": max(steps, 10)}
+    else:
+        n_steps = 64 if c["path"] == "grow" else steps
+        ms, fused_us, fused_pct = measure_fused(w, n_steps, warmup)
+        ctx_mid = w.L0 + (n_steps + 1) / 2 if c["path"] == "grow" else w.L0 + 1
+        alg = int(w.fused_bytes(ctx_mid))
+        r.update({
+            "path": "append 1 token x all layers (batched) + eakv_attention_fused_batch_device "
+                    "x all layers" + (", context growing over 64 steps" if c["path"] == "grow"
+                                      else ", context restored each step"),
+            "steps": n_steps,
+            "us_per_layer_step": round(ms * 1e3 / c["nl"], 3),
+            "fused_us_per_layer": round(fused_us, 3),
+            "fused_us_per_layer_min_median_max_over_steps": fused_pct,
+            "gbs": round(gbs(alg, fused_us), 1), "frac": round(gbs(alg, fused_us) / HBM_PEAK_GBS, 4),
+            "alg_bytes_per_layer_step": alg,
+        })
+        extra = {"ms_step": ms, "fused_us": fused_us, "alg": alg, "steps": n_steps}
+    r["quantize"] = {"gb_alg": round(w.quant_bytes / 1e9, 2), "ms": round(w.quant_ms, 3),
+                     "gbs": round(qgbs, 1), "frac": round(qgbs / HBM_PEAK_GBS, 4)}
+    log(f"bench: config {cid}: {r['us_per_layer_step']} us/layer-step, {r['gbs']} GB/s, "
+        f"quantize {qgbs:.0f} GB/s")
+    w.free()
+    H.synchronize()
+    if with_cpu:
+        log(f"bench: config {cid}: CPU baseline")
+        r["cpu"] = cpu_baseline(c, budget_s=8.0 if cid == HEADLINE else 5.0)
+        if c["path"] == "grow":
+            r["cpu_quantize"] = cpu_quantize_baseline(c)
+    return r, extra
+
+
+def reference_shapes_bench():
+    """The reference's own benchmark shapes (bench_libeakv.c:156-160: 1 layer
+    8 heads d128 at 2048 and 8192 tokens; 32 layers at 2048, measured on
+    layer 0) with its inputs (ramps (i % 2000)/200 - 5, queries 0.1) and
+    method (5 warmups, median of 20): the host-pointer eakv_attention_scores
+    and eakv_attention_output (PCIe copies and a stream wait included), the
+    device-pointer scores, and load_raw (2 warmups, median of 10); beside the
+    reference's published single-core K-score times (README.md:34-39)."""
+    import eakv_amd as E
+    from eakv_amd import hipmem as H
+    published = {(1, 2048): 210, (1, 8192): 844, (32, 2048): 213}
+    res = []
+    for nl, sl in ((1, 2048), (1, 8192), (32, 2048)):
+        nh, hd = 8, 128
+        data = ((np.arange(nl * 2 * nh * sl * hd, dtype=np.int32) % 2000).astype(np.float32)
+                / np.float32(200.0) - np.float32(5.0))
+        c = E.Cache(nl, nh, hd, sl)
+
+        def med(fn, warm, runs):
+            for _ in range(warm):
+                fn()
+            t = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                fn()
+                t.append(time.perf_counter() - t0)
+            return float(np.median(t)) * 1e6
+
+        t_load = med(lambda: c.load_raw(data, sl), 2, 10)
+        q = np.full((nh, hd), 0.1, np.float32)
+        scores = np.empty((nh, sl), np.float32)
+        wts = np.full((nh, sl), 1.0 / sl, np.float32)
+        out = np.empty((nh, hd), np.float32)
+        L = E.lib()
+        t_ks = med(lambda: L.eakv_attention_scores(c.h, q.ctypes.data, 0, nh, nh,
+                                                   scores.ctypes.data), 5, 20)
+        t_vs = med(lambda: L.eakv_attention_output(c.h, wts.ctypes.data, 0, nh, nh,
+                                                   out.ctypes.data), 5, 20)
+        dq = H.DeviceArray.from_host(q)
+        ds = H.DeviceArray((nh, sl))
+
+        def dev():
+            assert L.eakv_attention_scores_device(c.h, dq.ptr, 0, nh, nh, ds.ptr, None) == 0
+            c.sync()
+        t_dev = med(dev, 5, 20)
+        res.append({"shape": f"{nl} layer(s), 8 heads, d128, {sl} tokens",
+                    "published_cpu_k_score_us": published[(nl, sl)],
+                    "host_api_k_score_us": round(t_ks, 1), "host_api_v_output_us": round(t_vs, 1),
+                    "device_api_k_score_us_with_sync": round(t_dev, 1),
+                    "host_api_load_raw_us": round(t_load, 1)})
+        for a in (dq, ds):
+            a.free()
+        c.free()
+    return {"method": "bench_libeakv.c: inputs (i % 2000)/200 - 5, queries 0.1, median of 20 "
+                      "after 5 warmups (load_raw: 10 after 2), host clock; host_api_* include "
+                      "the H2D copy of the inputs, the D2H copy of the results and the wait",
+            "shapes": res}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=None, choices=sorted(CONFIGS),
+                    help="only this configuration (its own line as the headline)")
+    ap.add_argument("--ctx", type=int, default=None, help="override context length "
+                    "(with --config)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--unfused", action="store_true",
+                    help="with --config: only time the unfused K-score and V-sum calls, "
+                         "print their JSON line, then exit")
+    ap.add_argument("--dequant", action="store_true",
+                    help="only time whole-plane dequantization of the first cache of "
+                         "--config (default 4), print its JSON line, then exit")
+    ap.add_argument("--validate", action="store_true",
+                    help="only time the integrity check of the first cache, print its "
+                         "JSON line, then exit")
+    ap.add_argument("--ggml", action="store_true",
+                    help="only time the ggml block type's device functions on 1 GiB of "
+                         "f32 rows, print their JSON line, then exit")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB, 5 times (the "
+                         "known-size kernel for HBM byte counters), then exit")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
+              "sharding across GPUs is not built in this version", file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration << 20)
+        return
+    if args.ggml:
+        print(json.dumps(ggml_bench(max(1, args.steps), 2)), flush=True)
+        return
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)
+    if args.dequant or args.validate or args.unfused:
+        from eakv_amd import hipmem as H
+        w = Workload(args.config or HEADLINE, args.ctx)
+        w.fill_context()
+        w.prepare_step_inputs()
+        H.synchronize()
+        if args.dequant:
+            line = dequant_bench(w, max(1, args.steps // 4), 1)
+        elif args.validate:
+            line = validate_bench(w, max(3, args.steps), 2)
+        else:
+            line = unfused_bench(w, max(1, args.steps // 4), 1)
+        print(json.dumps(line), flush=True)
+        return
+
+    head_id = args.config or HEADLINE
+    ids = [args.config] if args.config else sorted(CONFIGS)
+    summaries, head = {}, None
+    for cid in ids:
+        r, extra = run_config(cid, args.steps if cid == head_id else max(5, args.steps // 2),
+                              args.warmup, args.ctx if args.config else None,
+                              with_cpu=not args.no_cpu, log=log)
+        summaries[str(cid)] = r
+        if cid == head_id:
+            head = (r, extra)
+    r, extra = head
+    c = CONFIGS[head_id]
+    line = {
+        "metric": metric_text(dict(c, L=args.ctx or c["L"])),
+        "value": r["us_per_layer_step"], "unit": "us/layer",
+        "n_gpus": 1, "steps": extra.get("steps", args.steps), "warmup": args.warmup,
+        "ms_per_step": round(extra["ms_step"], 4) if extra else None,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": DTYPE,
+        "data": "synthetic: seeded device generator, distributions of the configuration",
+        "config": {k: r[k] for k in ("workload", "layers", "q_heads", "kv_heads", "head_dim",
+                                     "context", "sequences", "path")},
+    }
+    if extra:
+        alg = extra["alg"]
+        read_gbs = read_peak(alg)
+        log(f"bench: plain streaming read of {alg / 1e6:.1f} MB passes: {read_gbs:.0f} GB/s")
+        traffic = None
+        tfile = os.path.join(ROOT, "profiles", f"fused_config{head_id}_traffic.json")
+        if os.path.exists(tfile):
+            traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+        achieved = gbs(alg, extra["fused_us"])
+        line.update({
+            "fused_us_per_layer": round(extra["fused_us"], 3),
+            "achieved_gbs": round(achieved, 1),
+            "quantize_gbs": r["quantize"]["gbs"],
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": traffic, "alg_bytes_per_launch": alg,
+                         "measured_read_gbs": round(read_gbs, 1),
+                         "frac_of_measured_read": round(achieved / read_gbs, 4)},
+        })
+    line["cpu_baseline"] = r.get("cpu")
+    line["configs"] = summaries
+    if not args.config:
+        log("bench: reference benchmark shapes (host-pointer API)")
+        line["reference_shapes"] = reference_shapes_bench()
+    print(json.dumps(line), flush=True)
+
+
+# ------------------------------------------------------ single-purpose modes
+
+def copy_calibration(n_bytes, reps=5):
+    """Copy n_bytes device-to-device `reps` times with the synth library's
+    streaming copy kernel; prints the bytes read and written per launch."""
+    from eakv_amd import hipmem as H
+    lib = Synth().lib
+    lib.eakv_synth_copy.restype = C.c_int
+    lib.eakv_synth_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
+    src = H.DeviceArray((n_bytes // 4,))
+    dst = H.DeviceArray((n_bytes // 4,))
+    e0, e1 = H.Event(), H.Event()
+    ms = []
+    for _ in range(reps):
+        e0.record(None)
+        rc = lib.eakv_synth_copy(dst.ptr, src.ptr, n_bytes, None)
+        if rc:
+            raise RuntimeError(f"copy launch failed: {rc}")
+        e1.record(None)
+        e1.synchronize()
+        ms.append(e0.elapsed_ms(e1))
+    print(json.dumps({"copy_bytes_read": n_bytes, "copy_bytes_written": n_bytes,
+                      "launches": reps, "ms": [round(m, 4) for m in ms],
+                      "gbs_read_plus_write": round(2 * n_bytes / min(ms) / 1e6, 1)}),
+          flush=True)
+
+
 def dequant_bench(w, steps, warmup):
     """Whole-plane dequantization (eakv_dequantize_range_device) of every
     (layer, kv) block of the first cache, back to back into one f32 buffer:
@@ -323,25 +792,16 @@ def dequant_bench(w, steps, warmup):
             rc = L.eakv_dequantize_range_device(cache.h, l, kv, 0, ng, out.ptr, None)
             assert rc == 0, E.last_error()
 
-    for _ in range(warmup):
-        one_pass()
-    H.synchronize()
-    e0, e1 = H.Event(), H.Event()
-    e0.record(w.stream)
-    for _ in range(steps):
-        one_pass()
-    e1.record(w.stream)
-    e1.synchronize()
-    us = e0.elapsed_ms(e1) * 1e3 / (steps * len(planes))
+    us = timed(H, w.stream, one_pass, steps, warmup, len(planes))
     alg = ng * (40 + 256)
-    gbs = alg / (us * 1e-6) / 1e9
+    g = gbs(alg, us)
     return {"metric": "plane dequantize to f32 GB/s (40 B read + 256 B written per group)",
-            "value": round(gbs, 1), "unit": "GB/s", "higher_is_better": True,
+            "value": round(g, 1), "unit": "GB/s", "higher_is_better": True,
             "us_per_plane": round(us, 3), "groups_per_plane": ng, "planes_per_step": len(planes),
             "steps": steps, "n_gpus": 1, "dtype": "q4_1 -> f32",
             "config": {"workload": c["name"], "plane": f"{c['nkv']} kv heads x {w.lmax} tokens x d{c['d']}"},
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "roofline": {"bound": "hbm", "achieved": round(g, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(g / HBM_PEAK_GBS, 4),
                          "alg_bytes_per_launch": alg}}
 
 
@@ -365,14 +825,14 @@ def validate_bench(w, steps, warmup):
     us = float(np.median(t)) * 1e6
     n = c["nkv"] * c["d"] * cache.seq_len // 64
     alg = 2 * c["nl"] * n * 8
-    gbs = alg / (us * 1e-6) / 1e9
+    g = gbs(alg, us)
     return {"metric": "integrity check GB/s (scale + bias read per group, whole host call)",
-            "value": round(gbs, 1), "unit": "GB/s", "higher_is_better": True,
+            "value": round(g, 1), "unit": "GB/s", "higher_is_better": True,
             "us_per_call": round(us, 1), "groups_per_block": n, "blocks": 2 * c["nl"],
             "codes": res.tolist()[:4], "steps": steps, "n_gpus": 1, "dtype": "f32 bit tests",
             "config": {"workload": c["name"]},
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "roofline": {"bound": "hbm", "achieved": round(g, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(g / HBM_PEAK_GBS, 4),
                          "alg_bytes_per_call": alg}}
 
 
@@ -405,195 +865,38 @@ def ggml_bench(steps, warmup, n_rows=65536, k=4096):
     }
     res = {}
     for name, (call, alg) in calls.items():
-        for _ in range(warmup):
-            assert call() == 0, E.last_error()
-        H.synchronize()
-        e0, e1 = H.Event(), H.Event()
-        e0.record(None)
-        for _ in range(steps):
-            assert call() == 0, E.last_error()
-        e1.record(None)
-        e1.synchronize()
-        us = e0.elapsed_ms(e1) * 1e3 / steps
-        gbs = alg / (us * 1e-6) / 1e9
-        res[name] = {"us_per_call": round(us, 2), "gbs": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes_per_call": alg}
+        def checked(call=call):
+            rc = call()
+            if rc:
+                raise RuntimeError(E.last_error())
+        us = timed(H, None, checked, steps, warmup, 1)
+        g = gbs(alg, us)
+        res[name] = {"us_per_call": round(us, 2), "gbs": round(g, 1),
+                     "frac": round(g / HBM_PEAK_GBS, 4), "alg_bytes_per_call": alg}
     return {"metric": "ggml block type device functions, GB/s of algorithmic bytes",
             "unit": "GB/s", "n_gpus": 1, "steps": steps, "dtype": "block_q4_1_eakv <-> f32",
             "config": {"rows": n_rows, "k": k, "bytes_f32": n * 4}, **res}
 
 
 def unfused_bench(w, steps, warmup):
-    """The reference API's unfused path on the first cache, every layer back
-    to back: eakv_attention_scores_device (k_score_kernel), then
-    eakv_attention_output_device (v_sum_kernel + chunk_sum_kernel) with
-    uniform weights 1/L (timing only; parity is the tests' job).  Returns the
-    JSON line with each call's mean time and GB/s of its algorithmic bytes:
-    K-score n_kv*L*gpd*40 + n_q*L*4 (scores) + n_q*d*4, V-sum
-    n_kv*L*gpd*40 + n_q*L*4 (weights) + n_q*d*4."""
-    E, H, c = w.E, w.H, w.cfg
-    cache = w.caches[0]
-    L = w.L0
-    nq, nkv, d = c["nq"], c["nkv"], c["d"]
-    scores = H.DeviceArray((nq, L))
-    wts = H.DeviceArray.from_host(np.full((nq, L), 1.0 / L, np.float32))
-    out = H.DeviceArray((nq, d))
-    lib = E.lib()
-
-    def run(which):
-        for l in range(c["nl"]):
-            q = w.ql[l].ptr                        # sequence 0's queries
-            if which == "k":
-                rc = lib.eakv_attention_scores_device(cache.h, q, l, nq, nkv, scores.ptr, None)
-            else:
-                rc = lib.eakv_attention_output_device(cache.h, wts.ptr, l, nq, nkv, out.ptr, None)
-            assert rc == 0, E.last_error()
-
-    res = {}
-    alg = nkv * L * (d // 64) * 40 + nq * L * 4 + nq * d * 4
-    for which, name in (("k", "k_score"), ("v", "v_sum")):
-        for _ in range(warmup):
-            run(which)
-        H.synchronize()
-        e0, e1 = H.Event(), H.Event()
-        e0.record(w.stream)
-        for _ in range(steps):
-            run(which)
-        e1.record(w.stream)
-        e1.synchronize()
-        us = e0.elapsed_ms(e1) * 1e3 / (steps * c["nl"])
-        res[name] = {"us_per_call": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
-                     "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "alg_bytes_per_call": alg}
-    return {"metric": "unfused K-score / V-sum per layer call, GB/s of algorithmic bytes",
-            "unit": "GB/s", "n_gpus": 1, "steps": steps, "dtype": "q4_1 (u8 nibbles + f32 scale/bias), f32 math",
-            "config": {"workload": c["name"], "layers": c["nl"], "q_heads": nq, "kv_heads": nkv,
-                       "head_dim": d, "context": L, "sequences": 1},
-            **res}
-
-
-def cpu_model():
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
-
-
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
-    ap.add_argument("--ctx", type=int, default=None, help="override context length")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--unfused", action="store_true",
-                    help="only time the unfused K-score and V-sum calls on the first "
-                         "cache, print their JSON line, then exit")
-    ap.add_argument("--dequant", action="store_true",
-                    help="only time whole-plane dequantization of the first cache, "
-                         "print its JSON line, then exit")
-    ap.add_argument("--validate", action="store_true",
-                    help="only time the integrity check of the first cache, print its "
-                         "JSON line, then exit")
-    ap.add_argument("--ggml", action="store_true",
-                    help="only time the ggml block type's device functions on 1 GiB of "
-                         "f32 rows, print their JSON line, then exit")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run a plain device copy of MIB MiB, 5 times (the "
-                         "known-size kernel for HBM byte counters), then exit")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); "
-              "sharding across GPUs is not built in this version", file=sys.stderr)
-        sys.exit(2)
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration << 20)
-        return
-    if args.ggml:
-        print(json.dumps(ggml_bench(max(1, args.steps), 2)), flush=True)
-        return
-
-    from eakv_amd import hipmem as H
-    log = lambda *a: print(*a, file=sys.stderr, flush=True)
-    w = Workload(args.config, args.ctx)
+    """The reference API's unfused calls on the first cache, every layer
+    back to back, each phase timed on its own: K-score, the caller's row
+    softmax, V-sum.  Returns the JSON line with each call's mean time and
+    GB/s of its algorithmic bytes (K-score n_kv*L*gpd*40 + n_q*L*4 + n_q*d*4,
+    softmax 2*n_q*L*4, V-sum n_kv*L*gpd*40 + n_q*L*4 + n_q*d*4)."""
     c = w.cfg
-    log(f"bench: config {args.config} {c['name']} ctx {w.L0 + 1}: filling caches")
-    w.fill_context()
-    w.prepare_step_inputs()
-    H.synchronize()
-    if args.dequant:
-        print(json.dumps(dequant_bench(w, max(1, args.steps // 4), 1)), flush=True)
-        return
-    if args.validate:
-        print(json.dumps(validate_bench(w, max(3, args.steps), 2)), flush=True)
-        return
-    if args.unfused:
-        print(json.dumps(unfused_bench(w, max(1, args.steps // 4), 1)), flush=True)
-        return
-    log(f"bench: quantize {w.quant_bytes / 1e9:.2f} GB alg in {w.quant_ms:.2f} ms "
-        f"({w.quant_bytes / w.quant_ms / 1e6:.0f} GB/s)")
-
-    for _ in range(args.warmup):
-        w.step()
-    H.synchronize()
-    # one event pair per step around its nl back-to-back fused calls: the
-    # steps run back to back, the host waits only after the last one
-    events = [[H.Event(), H.Event()] for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        w.step(events[k])
-    H.synchronize()
-    total_s = time.perf_counter() - t0
-    fused = np.array([e0.elapsed_ms(e1) / c["nl"] for e0, e1 in events])
-    fused_us = float(fused.mean() * 1e3)
-    alg = w.fused_bytes()
-    achieved = alg / (fused_us * 1e-6) / 1e9
-    ms_step = total_s / args.steps * 1e3
-    log(f"bench: {ms_step:.3f} ms/step, fused {fused_us:.2f} us/layer "
-        f"(min {fused.min() * 1e3:.2f}), {achieved:.0f} GB/s")
-
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"fused_config{args.config}_traffic.json")
-    if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
-
-    read_gbs = read_peak(alg)
-    log(f"bench: plain streaming read of {alg / 1e6:.1f} MB passes: {read_gbs:.0f} GB/s")
-
-    cpu = None
-    if not args.no_cpu:
-        log("bench: CPU baseline")
-        cpu = cpu_baseline(c)
-        cpu["cpu_model"] = cpu_model()
-
-    line = {
-        "metric": "fused Q4 attn µs/layer + achieved HBM GB/s, 32Q/8KV d128 32K ctx, 1 GPU",
-        "value": round(ms_step * 1e3 / c["nl"], 3),
-        "unit": "us/layer",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4_1 (u8 nibbles + f32 scale/bias), f32 math",
-        "data": "synthetic: seeded device generator, distributions of the configuration",
-        "config": {"workload": c["name"], "layers": c["nl"], "q_heads": c["nq"],
-                   "kv_heads": c["nkv"], "head_dim": c["d"], "context": w.L0 + 1,
-                   "sequences": c["nseq"],
-                   "step": "append 1 token x all layers (K,V) + fused attention x all layers"},
-        "fused_us_per_layer": round(fused_us, 3),
-        "achieved_gbs": round(achieved, 1),
-        "quantize_gbs": round(w.quant_bytes / w.quant_ms / 1e6, 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "alg_bytes_per_launch": alg,
-                     "measured_read_gbs": round(read_gbs, 1),
-                     "frac_of_measured_read": round(achieved / read_gbs, 4)},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line), flush=True)
+    u = measure_unfused(w, steps, warmup)
+    ks_b, sm_b, vs_b = w.unfused_bytes()
+    res = {}
+    for name, b in (("k_score", ks_b), ("softmax", sm_b), ("v_sum", vs_b)):
+        res[name] = {"us_per_call": round(u[name], 3), "gbs": round(gbs(b, u[name]), 1),
+                     "frac": round(gbs(b, u[name]) / HBM_PEAK_GBS, 4), "alg_bytes_per_call": b}
+    return {"metric": "unfused K-score / softmax / V-sum per layer call, GB/s of algorithmic bytes",
+            "unit": "GB/s", "n_gpus": 1, "steps": steps, "dtype": DTYPE,
+            "config": {"workload": c["name"], "layers": c["nl"], "q_heads": c["nq"],
+                       "kv_heads": c["nkv"], "head_dim": c["d"], "context": w.L0,
+                       "sequences": 1},
+            "step_us_per_layer": round(u["step"], 3), **res}
 
 
 if __name__ == "__main__":

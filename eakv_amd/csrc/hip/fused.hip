@@ -1026,16 +1026,23 @@ __global__ __launch_bounds__(D) void merge_kernel(
     const int n_tiles = (bt.seq_len[s] + kTT - 1) / kTT;
     const int n_chunks = min(max_chunks, (n_tiles + wpb - 1) / wpb);
     const float *p = part + ((int64_t)s * n_q + qh) * max_chunks * (D + 2);
+    // The (m, l) pair and o[i] of every chunk by vector buffer loads, all
+    // issued before any arithmetic: one memory round trip.  (As scalar
+    // loads the pairs overflow the scalar load counter, and the compiler's
+    // early waits split them into several round trips.)
+    const __amdgpu_buffer_rsrc_t r = plane_rsrc(p, (int64_t)max_chunks * (D + 2) * 4);
     float M = -1000000.0f * EAKV_LOG2E, lt = 0.0f, ot = 0.0f;
     for (int c0 = 0; c0 < n_chunks; c0 += kMergeBatch) {
         float m[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
 #pragma unroll
         for (int j = 0; j < kMergeBatch; j++) {
-            const float *pc = p + min(c0 + j, n_chunks - 1) * (D + 2);
-            m[j] = pc[0];
-            lv[j] = pc[1];
-            ov[j] = pc[2 + i];
+            const int so = min(c0 + j, n_chunks - 1) * (D + 2) * 4;
+            const auto ml = __builtin_amdgcn_raw_buffer_load_b64(r, 0, so, 0);
+            m[j] = __uint_as_float(ml[0]);
+            lv[j] = __uint_as_float(ml[1]);
+            ov[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, 4 * i, so + 8, 0));
         }
+        __builtin_amdgcn_sched_barrier(0);
         float Mn = M;
 #pragma unroll
         for (int j = 0; j < kMergeBatch; j++)

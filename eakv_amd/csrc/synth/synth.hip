@@ -106,7 +106,95 @@ __global__ __launch_bounds__(256) void read_kernel(const uint4 *__restrict__ src
     sink[tid] = a;
 }
 
+// The caller's row softmax of the reference's unfused workload (scores ->
+// softmax -> output; the reference leaves it to the caller): one block of
+// 1024 threads per row, w = exp(s - max) * (1 / sum), the max starting at
+// -1e6 as in the reference's fused kernel.  Rows of up to 16384 values stay
+// in registers (one read, one write); longer rows are read three times.
+// Used to time that workload, not for parity.
+__device__ __forceinline__ float block_max(float m, float *red)
+{
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+    for (int i = 1; i < 16; i++) m = fmaxf(m, red[i]);
+    __syncthreads();
+    return m;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red)
+{
+    for (int k = 32; k >= 1; k >>= 1) v += __shfl_xor(v, k, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+    for (int i = 1; i < 16; i++) v += red[i];
+    __syncthreads();
+    return v;
+}
+
+template <int PER>
+__global__ __launch_bounds__(1024) void softmax_kernel(const float *__restrict__ s,
+                                                       float *__restrict__ w, int L)
+{
+    __shared__ float red[16];
+    const float *r = s + (int64_t)blockIdx.x * L;
+    float *o = w + (int64_t)blockIdx.x * L;
+    const int t = threadIdx.x;
+    if constexpr (PER > 0) {
+        float v[PER];
+        float m = -1000000.0f;
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int i = t + 1024 * k;
+            v[k] = i < L ? r[i] : -INFINITY;
+            m = fmaxf(m, v[k]);
+        }
+        m = block_max(m, red);
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            v[k] = expf(v[k] - m);
+            sum += v[k];
+        }
+        const float inv = 1.0f / block_sum(sum, red);
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int i = t + 1024 * k;
+            if (i < L) o[i] = v[k] * inv;
+        }
+    } else {
+        float m = -1000000.0f;
+        for (int i = t; i < L; i += 1024) m = fmaxf(m, r[i]);
+        m = block_max(m, red);
+        float sum = 0.0f;
+        for (int i = t; i < L; i += 1024) sum += expf(r[i] - m);
+        const float inv = 1.0f / block_sum(sum, red);
+        for (int i = t; i < L; i += 1024) o[i] = expf(r[i] - m) * inv;
+    }
+}
+
 }  // namespace
+
+// Row softmax of scores[n_rows][L] into w (device pointers).
+extern "C" int eakv_synth_softmax(const float *scores, float *w, int n_rows, int L, void *stream)
+{
+    if (n_rows <= 0 || L <= 0) return 0;
+    const hipStream_t st = (hipStream_t)stream;
+    const dim3 g((unsigned)n_rows), b(1024);
+    if (L <= 2048)
+        hipLaunchKernelGGL(softmax_kernel<2>, g, b, 0, st, scores, w, L);
+    else if (L <= 4096)
+        hipLaunchKernelGGL(softmax_kernel<4>, g, b, 0, st, scores, w, L);
+    else if (L <= 8192)
+        hipLaunchKernelGGL(softmax_kernel<8>, g, b, 0, st, scores, w, L);
+    else if (L <= 16384)
+        hipLaunchKernelGGL(softmax_kernel<16>, g, b, 0, st, scores, w, L);
+    else
+        hipLaunchKernelGGL(softmax_kernel<0>, g, b, 0, st, scores, w, L);
+    return (int)hipGetLastError();
+}
 
 // Compute units of the current device (0 if the query fails).
 extern "C" int eakv_synth_cu_count(void)

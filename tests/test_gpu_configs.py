@@ -469,3 +469,22 @@ def test_gpu_loads_independently_built_file(E, rng, tmp_path):
         with pytest.raises(E.EakvError) as e:
             E.Cache.load(str(p))
         assert e.value.code == E.EAKV_ERR_FORMAT
+
+
+def test_bench_softmax_is_row_softmax(E, rng):
+    """The caller's row softmax the benchmark times for the unfused workloads
+    (libeakv_synth.so) against the oracle's, at every row length it uses
+    (register-resident up to 16384 values, three passes beyond)."""
+    from eakv_amd.hipmem import DeviceArray
+    lib = C.CDLL(os.path.join(ROOT, "eakv_amd", "libeakv_synth.so"))
+    lib.eakv_synth_softmax.restype = C.c_int
+    lib.eakv_synth_softmax.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+    for L in (1, 2048, 3000, 8192, 16384, 20000):
+        s = (rng.standard_normal((5, L)) * 4).astype(np.float32)
+        ds, dw = DeviceArray.from_host(s), DeviceArray((5, L))
+        assert lib.eakv_synth_softmax(ds.ptr, dw.ptr, 5, L, None) == 0
+        got = dw.download()
+        # two f32 summation orders of up to 20000 weights: 1e-4 relative
+        ok, err, nbad = tol_close(got, O.softmax_rows(s), 1e-7, 1e-4)
+        assert ok, (L, err, nbad)
+        assert abs(float(got.astype(np.float64).sum()) - 5.0) < 1e-3
