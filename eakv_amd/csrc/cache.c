@@ -58,6 +58,8 @@ void eakvd_geom_init(eakvd_geom *g, int n_layers, int n_kv_heads,
     g->s_off = round256(g->max_groups * 32);
     g->b_off = g->s_off + round256(g->max_groups * 4);
     g->block_bytes = g->b_off + round256(g->max_groups * 4);
+    g->ctr_off = g->block_bytes * 2 * n_layers + EAKVD_TAIL_PAD;
+    g->dev_bytes = g->ctr_off + (int64_t)n_kv_heads * EAKVD_CTR_STRIDE;
 }
 
 int eakvi_enter(const eakv_cache_t *c, int *prev)
@@ -194,7 +196,7 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
     c->head_dim = head_dim;
     c->max_seq_len = max_seq_len;
     eakvd_geom_init(&c->geom, n_layers, n_kv_heads, head_dim, max_seq_len);
-    c->dev_bytes = (size_t)c->geom.block_bytes * 2 * (size_t)n_layers + EAKVD_TAIL_PAD;
+    c->dev_bytes = (size_t)c->geom.dev_bytes;
 
     int e = eakvd_get_device(&c->device);
     if (e) goto hip_fail;
@@ -205,7 +207,8 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
     if (e) goto hip_fail;
     e = eakvd_malloc((void **)&c->dev, c->dev_bytes);
     if (e) goto hip_fail;
-    /* the reference calloc()s its planes (cache.c:33) */
+    /* the reference calloc()s its planes (cache.c:33); the counters start
+     * at zero */
     e = eakvd_memset_async(c->dev, 0, c->dev_bytes, c->stream);
     if (!e) e = eakvd_stream_sync(c->stream);
     if (e) goto hip_fail;

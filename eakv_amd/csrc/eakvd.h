@@ -9,6 +9,9 @@
  *   group index inside a plane = h*gph + t*gpd + j  (gph = max_seq_len*gpd,
  *   gpd = head_dim/64), the indexing of reference src/cache.c:69,:137 and
  *   src/attention.c:7.  Block and plane starts are rounded up to 256 bytes.
+ *   After the last block: EAKVD_TAIL_PAD bytes, then at ctr_off one chunk
+ *   counter per kv head, EAKVD_CTR_STRIDE bytes apart (the unfused V-sum's;
+ *   zero between calls).
  */
 #ifndef EAKVD_H
 #define EAKVD_H
@@ -28,6 +31,10 @@ extern "C" {
  * sequence's last token and masks them. */
 #define EAKVD_TAIL_PAD (64 * 1024)
 
+/* Bytes between two chunk counters: counters on separate 64-byte lines do
+ * not serialize one another's atomics. */
+#define EAKVD_CTR_STRIDE 64
+
 typedef struct {
     int     n_layers, n_kv_heads, head_dim, max_seq_len;
     int64_t gpd;          /* groups per token per head */
@@ -35,6 +42,8 @@ typedef struct {
     int64_t max_groups;   /* groups per plane */
     int64_t s_off, b_off; /* plane offsets inside a block, bytes */
     int64_t block_bytes;  /* bytes per (layer, kv) block */
+    int64_t ctr_off;      /* chunk counters, after the blocks and the tail pad */
+    int64_t dev_bytes;    /* the whole device allocation */
 } eakvd_geom;
 
 void eakvd_geom_init(eakvd_geom *g, int n_layers, int n_kv_heads,

@@ -34,6 +34,19 @@ __device__ __forceinline__ uint32_t byte_of(const uint4 &v, int i)
     return (w >> (8 * (i & 3))) & 0xffu;
 }
 
+// Byte J of x as a float, one v_cvt_f32_ubyteJ (the compiler otherwise
+// extracts the byte with a separate v_bfe_u32 first).
+template <int J>
+__device__ __forceinline__ float ubyte_f32(uint32_t x)
+{
+    float r;
+    if constexpr (J == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+    else if constexpr (J == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+    else if constexpr (J == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
 // Reference reduce_add over 16 lanes, pairwise halving tree (the order the
 // CPU restatement fixes): v8[i]=a[i]+a[i+8], v4, v2, then v2[0]+v2[1].
 __device__ __forceinline__ float reduce16(const float *a)

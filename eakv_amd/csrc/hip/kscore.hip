@@ -21,18 +21,14 @@
 
 namespace {
 
-// Byte J of x as a float, one v_cvt_f32_ubyteJ (the compiler otherwise
-// extracts the byte with a separate v_bfe_u32 first).
-template <int J>
-__device__ __forceinline__ float ubyte_f32(uint32_t x)
-{
-    float r;
-    if constexpr (J == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
-    else if constexpr (J == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
-    else if constexpr (J == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
-    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
-    return r;
-}
+#ifndef EAKV_KS_BUFS
+#define EAKV_KS_BUFS 2
+#endif
+#ifndef EAKV_KS_BLOCKS_PER_CU
+#define EAKV_KS_BLOCKS_PER_CU 2
+#endif
+constexpr int kKsBufs = EAKV_KS_BUFS;               // slices per wave in flight, one consumed
+constexpr int kKsBlocksPerCU = EAKV_KS_BLOCKS_PER_CU;
 
 template <int J>
 __device__ __forceinline__ void dequant4(float *klo, float *khi, uint32_t lo, uint32_t hi,
@@ -88,8 +84,8 @@ __device__ __forceinline__ void k_load(const uint8_t *w, const float *sc, const 
 
 // Block b takes the 256-token slices b, b + gridDim.x, ... of its kv head
 // (one token per lane) and loads the next slice while it computes one.
-template <int D>
-__global__ __launch_bounds__(256) void k_score_kernel(
+template <int D, bool MHA>
+__device__ __forceinline__ void k_score_body(
     const uint8_t *__restrict__ kw, const float *__restrict__ ks,
     const float *__restrict__ kb, int64_t gph, int L,
     const float *__restrict__ q, int qpk, float *__restrict__ scores, float rs)
@@ -107,6 +103,40 @@ __global__ __launch_bounds__(256) void k_score_kernel(
     // with every q head of the kv head
     auto compute = [&](const KTok<D> &T, int sl) {
         const int t = sl * 256 + threadIdx.x;
+        if constexpr (MHA) {
+            // one q head: each dequantized value goes straight into its fma,
+            // chunks c = 4*grp + 2*nib + half in order
+            float acc[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+            // q is read through the scalar cache per slice: the compiler
+            // barrier keeps it from holding all D values in vector registers
+            // across slices
+            const float *qh = qk;
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int grp = 0; grp < GPD; grp++)
+#pragma unroll
+                for (int nib = 0; nib < 2; nib++)
+#pragma unroll
+                    for (int half = 0; half < 2; half++) {
+                        const uint4 v = T.raw[grp * 2 + half];
+                        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+                        const float *qc = qh + (4 * grp + 2 * nib + half) * 16;
+#pragma unroll
+                        for (int wd = 0; wd < 4; wd++) {
+                            const uint32_t n = (nib ? w4[wd] >> 4 : w4[wd]) & 0x0f0f0f0fu;
+                            float *a = &acc[4 * wd];
+                            const float s = T.sc[grp], b = T.bi[grp];
+                            a[0] = fmaf(fmaf(ubyte_f32<0>(n), s, b), qc[4 * wd + 0], a[0]);
+                            a[1] = fmaf(fmaf(ubyte_f32<1>(n), s, b), qc[4 * wd + 1], a[1]);
+                            a[2] = fmaf(fmaf(ubyte_f32<2>(n), s, b), qc[4 * wd + 2], a[2]);
+                            a[3] = fmaf(fmaf(ubyte_f32<3>(n), s, b), qc[4 * wd + 3], a[3]);
+                        }
+                    }
+            if (t < L) scores[(int64_t)kvh * L + t] = __fmul_rn(reduce16(acc), rs);
+            return;
+        }
         // k[c*16 + i]: chunk c = 4*grp + 2*nib + half, byte i of half `half`
         float k[D];
 #pragma unroll
@@ -142,25 +172,48 @@ __global__ __launch_bounds__(256) void k_score_kernel(
         }
     };
 
-    // two buffers in turn: the next slice loads into one while the other is
+    // kKsBufs buffers in turn: the next kKsBufs - 1 slices load while one is
     // consumed (no copies between them, so the consumer waits only for its
-    // own loads)
+    // own loads).  The loads past the last slice are unconditional (past the
+    // end they read 0 and cost no memory traffic), so every path waits for
+    // the same loads.
     const int G = gridDim.x;
-    KTok<D> b0, b1;
+    KTok<D> buf[kKsBufs];
     int sl = blockIdx.x;
-    // the loads of the next slice are unconditional (past the end they read
-    // 0 and cost no memory traffic), so every path waits for the same loads
-    k_load<D>(hw, hs, hbi, L, sl, b0);
+#pragma unroll
+    for (int i = 0; i < kKsBufs - 1; i++) k_load<D>(hw, hs, hbi, L, sl + i * G, buf[i]);
     for (;;) {
-        k_load<D>(hw, hs, hbi, L, sl + G, b1);
-        compute(b0, sl);
-        sl += G;
-        if (sl >= n_sl) break;
-        k_load<D>(hw, hs, hbi, L, sl + G, b0);
-        compute(b1, sl);
-        sl += G;
-        if (sl >= n_sl) break;
+#pragma unroll
+        for (int j = 0; j < kKsBufs; j++) {
+            k_load<D>(hw, hs, hbi, L, sl + (kKsBufs - 1) * G, buf[(j + kKsBufs - 1) % kKsBufs]);
+            compute(buf[j], sl);
+            sl += G;
+            if (sl >= n_sl) return;
+        }
     }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_score_kernel(
+    const uint8_t *__restrict__ kw, const float *__restrict__ ks,
+    const float *__restrict__ kb, int64_t gph, int L,
+    const float *__restrict__ q, int qpk, float *__restrict__ scores, float rs)
+{
+    k_score_body<D, false>(kw, ks, kb, gph, L, q, qpk, scores, rs);
+}
+
+#ifndef EAKV_KS_MHA_WAVES
+#define EAKV_KS_MHA_WAVES 2
+#endif
+// One q head per kv head: registers for EAKV_KS_MHA_WAVES waves per SIMD.
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EAKV_KS_MHA_WAVES)))
+void k_score_mha_kernel(
+    const uint8_t *__restrict__ kw, const float *__restrict__ ks,
+    const float *__restrict__ kb, int64_t gph, int L,
+    const float *__restrict__ q, int qpk, float *__restrict__ scores, float rs)
+{
+    k_score_body<D, true>(kw, ks, kb, gph, L, q, qpk, scores, rs);
 }
 
 // Blocks per kv head: two waves per SIMD over the chip, at most one per
@@ -175,7 +228,7 @@ int k_blocks(int n_sl, int n_kv)
                            hipSuccess && v > 0
                    ? v : 256;
     }
-    const int want = (2 * n_cu + n_kv - 1) / n_kv;
+    const int want = (kKsBlocksPerCU * n_cu + n_kv - 1) / n_kv;
     return want < n_sl ? want : n_sl;
 }
 
@@ -191,11 +244,9 @@ extern "C" int eakvd_k_score(const eakvd_geom *g, const uint8_t *base,
     const dim3 grid((unsigned)k_blocks(ceil_div_i(seq_len, 256), n_kv), (unsigned)n_kv);
     const int qpk = n_q / n_kv;
     const float rs = 1.0f / sqrtf((float)g->head_dim);
-    if (g->head_dim == 64)
-        hipLaunchKernelGGL(k_score_kernel<64>, grid, dim3(256), 0, st, p.w,
-                           p.s, p.b, g->gph, seq_len, q, qpk, scores, rs);
-    else
-        hipLaunchKernelGGL(k_score_kernel<128>, grid, dim3(256), 0, st, p.w,
-                           p.s, p.b, g->gph, seq_len, q, qpk, scores, rs);
+    auto kern = g->head_dim == 64 ? (qpk == 1 ? k_score_mha_kernel<64> : k_score_kernel<64>)
+                                  : (qpk == 1 ? k_score_mha_kernel<128> : k_score_kernel<128>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, p.w, p.s, p.b, g->gph, seq_len, q, qpk,
+                       scores, rs);
     return (int)hipGetLastError();
 }

@@ -9,21 +9,190 @@
 // added in a fixed order, so results are deterministic and agree with the
 // single chain to rounding.
 //
-// Layout: a lane owns one packed dword of a token (8 dims: 4 low nibbles and
-// the 4 high nibbles 32 dims further), D/8 lanes per token, 256/(D/8) token
-// slots per block.  V is dequantized once per token and reused by every q
-// head of its group (HP per pass: 1, 2, 4 or 8, the smallest that covers
-// the group up to 8, so registers are spent only on heads that exist).  A lane takes kBatch tokens of its
-// slot at a time and issues all their loads (V word, scale, bias, weights)
-// before the arithmetic, so kBatch loads per lane are in flight; a block
-// covers a chunk of kChunk tokens of one kv head and writes one partial per
-// q head, which chunk_sum_kernel adds in a fixed order.
+// Two programs; each block covers a chunk of tokens of one kv head and writes
+// one partial per q head, and the partials are added in a fixed order.
+//
+// v_sum_mha_kernel (one q head per kv head): a lane owns 16 packed bytes of a
+//   token (32 dims: 16 low nibbles and the 16 high nibbles 32 dims further),
+//   D/32 lanes per token, so a wave's load of one 16-byte unit per lane reads
+//   1 KB of consecutive tokens.  The planes and the weight row are addressed
+//   through buffer resources that end at the chunk's last token: reads past
+//   it return 0 and add fma(0, 0, o) = o, so every lane runs the same
+//   iterations without bounds tests.  Nibbles become floats by masking a
+//   dword to four byte-wide nibbles and converting its bytes.  The last
+//   block of a kv head adds the chunk partials (no second launch).
+// v_sum_kernel (groups of q heads): a lane owns one packed dword of a token
+//   (8 dims), D/8 lanes per token, 256/(D/8) token slots per block.  V is
+//   dequantized once per token and reused by every q head of its group (HP
+//   per pass: 1, 2, 4 or 8, the smallest that covers the group up to 8, so
+//   registers are spent only on heads that exist).  chunk_sum_kernel adds
+//   the partials.
+// A lane takes a batch of tokens of its slot at a time and issues all their
+// loads (V bytes, scale, bias, weights) before the arithmetic.
 #include "common.h"
 
 namespace {
 
 constexpr int kBatch = 8;
 constexpr int kChunk = 256;
+
+#ifndef EAKV_VSUM_MHA_BATCH
+#define EAKV_VSUM_MHA_BATCH 8
+#endif
+constexpr int kMhaBatch = EAKV_VSUM_MHA_BATCH;   // tokens per lane per batch
+
+template <int D>
+struct MhaGeo {
+    static constexpr int GPD = D / 64;
+    static constexpr int RB = D / 2;               // packed bytes of a token
+    static constexpr int LPT = D / 32;             // lanes per token
+    static constexpr int TS = 256 / LPT;           // token slots per block
+    static constexpr int PAD = 4;                  // floats between slot rows in LDS
+    static constexpr int STEP = TS * kMhaBatch;    // tokens per batch of a block
+};
+
+// Partials cross blocks through device-scope (sc1) stores and loads: they
+// write through to, and read from, the device's coherence point, so no L2
+// writeback or invalidate (a whole-cache operation per XCD, costlier than
+// the kernel when every block pays it) is needed between blocks.
+__device__ __forceinline__ void st_dev(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p)
+{
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block (ch, kvh): tokens [ch*chunk, min(L, ch*chunk + chunk)) of kv head kvh
+// (= q head kvh), weights w[kvh][t].  With one chunk the block writes
+// out[kvh][D]; otherwise it writes partial[ch][kvh][D], counts itself on the
+// kv head's counter (ctr + kvh*EAKVD_CTR_STRIDE bytes), and the block that
+// counts last adds the chunks' partials in chunk order into out and sets the
+// counter back to zero for the next call (no other block of the launch
+// touches it again).
+template <int D>
+__global__ __launch_bounds__(256) void v_sum_mha_kernel(
+    const uint8_t *__restrict__ vw, const float *__restrict__ vs,
+    const float *__restrict__ vb, int64_t gph, int L,
+    const float *__restrict__ w, int chunk, int n_q, float *__restrict__ partial,
+    float *__restrict__ out, uint8_t *__restrict__ ctr)
+{
+    using G = MhaGeo<D>;
+    __shared__ float red[G::TS * (D + G::PAD)];
+
+    const int kvh = blockIdx.y, ch = blockIdx.x;
+    const int qq = threadIdx.x % G::LPT, ts = threadIdx.x / G::LPT;
+    const int t_begin = ch * chunk;
+    const int n_t = min(L - t_begin, chunk);      // >= 1: the grid covers L
+    const int64_t g0 = (int64_t)kvh * gph + (int64_t)t_begin * G::GPD;
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(vw + g0 * 32),
+                                                      (short)0, n_t * G::RB, 0x00020000);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(vs + g0), (short)0,
+                                                      n_t * G::GPD * 4, 0x00020000);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(vb + g0), (short)0,
+                                                      n_t * G::GPD * 4, 0x00020000);
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(w + (int64_t)kvh * L + t_begin), (short)0, n_t * 4, 0x00020000);
+    // this lane's bytes of a token: 16*qq..16*qq+15 of the row, in group qq/2
+    const int vo = ts * G::RB + 16 * qq;
+    const int so = (ts * G::GPD + qq / 2) * 4;
+    const int wo = ts * 4;
+
+    float acc[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) acc[i] = 0.0f;
+
+    for (int base = 0; base < n_t; base += G::STEP) {
+        v4i raw[kMhaBatch];
+        float sc[kMhaBatch], bi[kMhaBatch], wt[kMhaBatch];
+#pragma unroll
+        for (int u = 0; u < kMhaBatch; u++) {
+            const int t = base + u * G::TS;       // the slot's token, less ts
+            // whole offsets in the range-checked vector operand
+            raw[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + t * G::RB, 0, 0);
+            sc[u] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rs, so + t * G::GPD * 4, 0, 0));
+            bi[u] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rb, so + t * G::GPD * 4, 0, 0));
+            wt[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, wo + t * 4, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kMhaBatch; u++) {
+#pragma unroll
+            for (int wd = 0; wd < 4; wd++) {
+                const uint32_t x = (uint32_t)raw[u][wd];
+                const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+                float *al = &acc[4 * wd], *ah = &acc[16 + 4 * wd];
+                al[0] = fmaf(fmaf(ubyte_f32<0>(lo), sc[u], bi[u]), wt[u], al[0]);
+                ah[0] = fmaf(fmaf(ubyte_f32<0>(hi), sc[u], bi[u]), wt[u], ah[0]);
+                al[1] = fmaf(fmaf(ubyte_f32<1>(lo), sc[u], bi[u]), wt[u], al[1]);
+                ah[1] = fmaf(fmaf(ubyte_f32<1>(hi), sc[u], bi[u]), wt[u], ah[1]);
+                al[2] = fmaf(fmaf(ubyte_f32<2>(lo), sc[u], bi[u]), wt[u], al[2]);
+                ah[2] = fmaf(fmaf(ubyte_f32<2>(hi), sc[u], bi[u]), wt[u], ah[2]);
+                al[3] = fmaf(fmaf(ubyte_f32<3>(lo), sc[u], bi[u]), wt[u], al[3]);
+                ah[3] = fmaf(fmaf(ubyte_f32<3>(hi), sc[u], bi[u]), wt[u], ah[3]);
+            }
+        }
+    }
+
+    // slot rows in LDS: low nibble i -> dim 64*(qq/2) + 16*(qq%2) + i, high +32
+    float *r = red + ts * (D + G::PAD) + 64 * (qq / 2) + 16 * (qq % 2);
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+        *reinterpret_cast<float4 *>(r + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+        *reinterpret_cast<float4 *>(r + 32 + i) =
+            make_float4(acc[16 + i], acc[17 + i], acc[18 + i], acc[19 + i]);
+    }
+    __syncthreads();
+    // thread (part, dim) adds TS/P slot rows in order, then part 0 adds the P sums
+    constexpr int P = 256 / D;
+    constexpr int RPP = G::TS / P;
+    const int dim = threadIdx.x % D, part = threadIdx.x / D;
+    float sum = red[part * RPP * (D + G::PAD) + dim];
+#pragma unroll 8
+    for (int k = 1; k < RPP; k++) sum = __fadd_rn(sum, red[(part * RPP + k) * (D + G::PAD) + dim]);
+    __syncthreads();
+    red[part * D + dim] = sum;
+    __syncthreads();
+    const int nc = gridDim.x;
+    if (part == 0) {
+        float t = red[dim];
+#pragma unroll
+        for (int k = 1; k < P; k++) t = __fadd_rn(t, red[k * D + dim]);
+        if (nc == 1)
+            out[(int64_t)kvh * D + dim] = t;
+        else
+            st_dev(&partial[((int64_t)ch * n_q + kvh) * D + dim], t);
+    }
+    if (nc == 1) return;
+
+    // every thread's partial store is complete (vmcnt 0) before the barrier,
+    // and so before the count; the last block reads the partials after it
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int last;
+    unsigned *uc = reinterpret_cast<unsigned *>(ctr + (int64_t)kvh * EAKVD_CTR_STRIDE);
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(uc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(nc - 1);
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x == 0) __hip_atomic_store(uc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < D) {
+        float sum = 0.0f;
+        for (int c0 = 0; c0 < nc; c0 += 16) {
+            float p[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                p[j] = ld_dev(&partial[((int64_t)min(c0 + j, nc - 1) * n_q + kvh) * D + threadIdx.x]);
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (c0 + j < nc) sum = __fadd_rn(sum, p[j]);
+        }
+        out[(int64_t)kvh * D + threadIdx.x] = sum;
+    }
+}
 
 template <int D, int HP>
 __global__ __launch_bounds__(256) void v_sum_kernel(
@@ -158,6 +327,27 @@ __global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ out, int6
     if (i < n) out[i] = 0.0f;
 }
 
+// Tokens per block of the MHA program: whole batches, one batch per block
+// until the grid holds about 4 blocks per CU (4 waves per SIMD), at most
+// 2^20 tokens (the 32-bit offsets of the chunk's resources).
+int mha_chunk(int D, int L, int n_kv)
+{
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, v = 0;
+        n_cu = hipGetDevice(&dev) == hipSuccess &&
+                       hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                           hipSuccess && v > 0
+                   ? v : 256;
+    }
+    const int step = D == 64 ? MhaGeo<64>::STEP : MhaGeo<128>::STEP;
+    const int64_t blocks = (int64_t)n_kv * ceil_div_i(L, step);
+    int64_t it = blocks / (4 * (int64_t)n_cu);
+    const int64_t it_max = (1 << 20) / step;
+    it = it < 1 ? 1 : (it > it_max ? it_max : it);
+    return (int)(step * it);
+}
+
 }  // namespace
 
 extern "C" size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len,
@@ -186,9 +376,22 @@ extern "C" int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base,
     const int r = eakvd_v_sum_mfma(g, base, layer, seq_len, w, n_q, n_kv, out, work, stream);
     if (r >= 0) return r;
     const Planes p = planes_of(*g, base, layer, 1);
-    const int n_chunks = ceil_div_i(seq_len, kChunk);
     const int qpk = n_q / n_kv;
     float *partial = (float *)work;
+    if (qpk == 1) {
+        const int chunk = mha_chunk(g->head_dim, seq_len, n_kv);
+        const int nc = ceil_div_i(seq_len, chunk);
+        const dim3 grid((unsigned)nc, (unsigned)n_kv);
+        uint8_t *ctr = const_cast<uint8_t *>(base) + g->ctr_off;
+        if (g->head_dim == 64)
+            hipLaunchKernelGGL(v_sum_mha_kernel<64>, grid, dim3(256), 0, st, p.w, p.s, p.b,
+                               g->gph, seq_len, w, chunk, n_q, partial, out, ctr);
+        else
+            hipLaunchKernelGGL(v_sum_mha_kernel<128>, grid, dim3(256), 0, st, p.w, p.s, p.b,
+                               g->gph, seq_len, w, chunk, n_q, partial, out, ctr);
+        return (int)hipGetLastError();
+    }
+    const int n_chunks = ceil_div_i(seq_len, kChunk);
     const dim3 grid((unsigned)n_chunks, (unsigned)n_kv);
     auto kern = g->head_dim == 64
                     ? (qpk <= 1 ? v_sum_kernel<64, 1> : qpk <= 2 ? v_sum_kernel<64, 2>
