@@ -75,6 +75,10 @@ constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 unit
 #define EAKV_FUSED_SLOTS 3
 #endif
 constexpr int kSlots = EAKV_FUSED_SLOTS;  // load groups per wave: one consumed, the rest in flight
+#ifndef EAKV_SHARE_Q
+#define EAKV_SHARE_Q 1
+#endif
+constexpr bool kShareQ = EAKV_SHARE_Q;    // one wave per quad computes the q operands
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void *lds_ptr;
@@ -467,9 +471,10 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // pa = i%4), k-block qq = l/16; k-slot j of group gg holds dim
     // 64gg + 8qq + j (j < 8, low nibbles) or 64gg + 32 + 8qq + (j-8).
     // Quad hq holds heads 4hq..4hq+3.  Rows of heads >= G are zero (their q
-    // is read from head 0 and dropped).  The q loads are issued first, then
-    // the first two load groups (further below), so the digit arithmetic
-    // waits only for q.
+    // is read from head 0 and dropped).  Every wave of the block serves the
+    // same heads, so wave hq alone computes quad hq's operands and shares
+    // them through LDS.  The q loads are issued first, then the first two
+    // load groups (further below), so the digit arithmetic waits only for q.
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
     bool qrow[HH];
     float qv[HH][GPD][16];
@@ -477,6 +482,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
 #pragma unroll
     for (int hq = 0; hq < HH; hq++) {
         qrow[hq] = 4 * hq + ha < G;
+        if (kShareQ && w != hq) continue;
         const float4 *qh4 = (const float4 *)(qs + (qrow[hq] ? 4 * hq + ha : 0) * D);
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
@@ -644,6 +650,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     if constexpr (!VS)
 #pragma unroll
     for (int hq = 0; hq < HH; hq++) {
+    if (kShareQ && w != hq) continue;
     float amax = 0.0f;
     float qsum[GPD];
 #pragma unroll
@@ -688,6 +695,42 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     kwh[hq] = ldexpf(rs2, 16 - esh_o);
 #pragma unroll
     for (int gg = 0; gg < GPD; gg++) bq[hq][gg] = rs2 * __shfl(qsum[gg], 4 * ho, 64);
+    }
+    if constexpr (!VS && kShareQ) {
+        // quad hq's operands of lane l: dwords (hq*QR + f)*64 + l of the
+        // digit rows, which no wave uses before its first tile's weights
+        constexpr int QR = GPD * 4 + 2 + GPD;
+        static_assert(HH * QR * 64 * 4 <= (int)sizeof(z_lds), "operands fit the digit rows");
+        uint32_t *xq = reinterpret_cast<uint32_t *>(&z_lds[0][0]);
+#pragma unroll
+        for (int hq = 0; hq < HH; hq++) {
+            if (w != hq) continue;
+            uint32_t *x = xq + hq * QR * 64 + l;
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+                for (int w4 = 0; w4 < 4; w4++) x[(gg * 4 + w4) * 64] = (uint32_t)A[hq][gg][w4];
+            x[GPD * 4 * 64] = __float_as_uint(kwl[hq]);
+            x[(GPD * 4 + 1) * 64] = __float_as_uint(kwh[hq]);
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) x[(GPD * 4 + 2 + gg) * 64] = __float_as_uint(bq[hq][gg]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int hq = 0; hq < HH; hq++) {
+            if (w == hq) continue;
+            const uint32_t *x = xq + hq * QR * 64 + l;
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++)
+#pragma unroll
+                for (int w4 = 0; w4 < 4; w4++) A[hq][gg][w4] = (int)x[(gg * 4 + w4) * 64];
+            kwl[hq] = __uint_as_float(x[GPD * 4 * 64]);
+            kwh[hq] = __uint_as_float(x[(GPD * 4 + 1) * 64]);
+#pragma unroll
+            for (int gg = 0; gg < GPD; gg++) bq[hq][gg] = __uint_as_float(x[(GPD * 4 + 2 + gg) * 64]);
+        }
+        // every wave has its operands before any wave writes digit rows
+        __syncthreads();
     }
 
     WaveState<D> S[HH];
