@@ -36,19 +36,16 @@ namespace {
 constexpr int kBatch = 8;
 constexpr int kChunk = 256;
 
-#ifndef EAKV_VSUM_MHA_BATCH
-#define EAKV_VSUM_MHA_BATCH 8
-#endif
-constexpr int kMhaBatch = EAKV_VSUM_MHA_BATCH;   // tokens per lane per batch
-
-template <int D>
+// Tokens per lane per batch: 8 where the grid still fills the chip with 8,
+// else 2 (short contexts: more blocks, less serial work per lane).
+template <int D, int KB>
 struct MhaGeo {
     static constexpr int GPD = D / 64;
     static constexpr int RB = D / 2;               // packed bytes of a token
     static constexpr int LPT = D / 32;             // lanes per token
     static constexpr int TS = 256 / LPT;           // token slots per block
     static constexpr int PAD = 4;                  // floats between slot rows in LDS
-    static constexpr int STEP = TS * kMhaBatch;    // tokens per batch of a block
+    static constexpr int STEP = TS * KB;           // tokens per batch of a block
 };
 
 // Partials cross blocks through device-scope (sc1) stores and loads: they
@@ -71,14 +68,14 @@ __device__ __forceinline__ float ld_dev(const float *p)
 // counts last adds the chunks' partials in chunk order into out and sets the
 // counter back to zero for the next call (no other block of the launch
 // touches it again).
-template <int D>
+template <int D, int KB>
 __global__ __launch_bounds__(256) void v_sum_mha_kernel(
     const uint8_t *__restrict__ vw, const float *__restrict__ vs,
     const float *__restrict__ vb, int64_t gph, int L,
     const float *__restrict__ w, int chunk, int n_q, float *__restrict__ partial,
     float *__restrict__ out, uint8_t *__restrict__ ctr)
 {
-    using G = MhaGeo<D>;
+    using G = MhaGeo<D, KB>;
     __shared__ float red[G::TS * (D + G::PAD)];
 
     const int kvh = blockIdx.y, ch = blockIdx.x;
@@ -104,10 +101,10 @@ __global__ __launch_bounds__(256) void v_sum_mha_kernel(
     for (int i = 0; i < 32; i++) acc[i] = 0.0f;
 
     for (int base = 0; base < n_t; base += G::STEP) {
-        v4i raw[kMhaBatch];
-        float sc[kMhaBatch], bi[kMhaBatch], wt[kMhaBatch];
+        v4i raw[KB];
+        float sc[KB], bi[KB], wt[KB];
 #pragma unroll
-        for (int u = 0; u < kMhaBatch; u++) {
+        for (int u = 0; u < KB; u++) {
             const int t = base + u * G::TS;       // the slot's token, less ts
             // whole offsets in the range-checked vector operand
             raw[u] = __builtin_amdgcn_raw_buffer_load_b128(rw, vo + t * G::RB, 0, 0);
@@ -118,7 +115,7 @@ __global__ __launch_bounds__(256) void v_sum_mha_kernel(
             wt[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, wo + t * 4, 0, 0));
         }
 #pragma unroll
-        for (int u = 0; u < kMhaBatch; u++) {
+        for (int u = 0; u < KB; u++) {
 #pragma unroll
             for (int wd = 0; wd < 4; wd++) {
                 const uint32_t x = (uint32_t)raw[u][wd];
@@ -327,10 +324,16 @@ __global__ __launch_bounds__(256) void zero_kernel(float *__restrict__ out, int6
     if (i < n) out[i] = 0.0f;
 }
 
-// Tokens per block of the MHA program: whole batches, one batch per block
-// until the grid holds about 4 blocks per CU (4 waves per SIMD), at most
-// 2^20 tokens (the 32-bit offsets of the chunk's resources).
-int mha_chunk(int D, int L, int n_kv)
+// Launch shape of the MHA program: batches of 8 tokens per lane where one
+// batch per block gives at least one block per CU, else of 2; tokens per
+// block: whole batches, one batch per block until the grid holds about 4
+// blocks per CU (4 waves per SIMD), at most 2^20 tokens (the 32-bit offsets
+// of the chunk's resources).
+struct MhaPlan {
+    int kb, chunk, nc;
+};
+
+MhaPlan mha_plan(int D, int L, int n_kv)
 {
     static int n_cu = 0;
     if (n_cu == 0) {
@@ -340,12 +343,17 @@ int mha_chunk(int D, int L, int n_kv)
                            hipSuccess && v > 0
                    ? v : 256;
     }
-    const int step = D == 64 ? MhaGeo<64>::STEP : MhaGeo<128>::STEP;
+    const int ts = D == 64 ? MhaGeo<64, 8>::TS : MhaGeo<128, 8>::TS;
+    MhaPlan p;
+    p.kb = (int64_t)n_kv * ceil_div_i(L, ts * 8) >= n_cu ? 8 : 2;
+    const int step = ts * p.kb;
     const int64_t blocks = (int64_t)n_kv * ceil_div_i(L, step);
     int64_t it = blocks / (4 * (int64_t)n_cu);
     const int64_t it_max = (1 << 20) / step;
     it = it < 1 ? 1 : (it > it_max ? it_max : it);
-    return (int)(step * it);
+    p.chunk = (int)(step * it);
+    p.nc = ceil_div_i(L, p.chunk);
+    return p;
 }
 
 }  // namespace
@@ -355,7 +363,11 @@ extern "C" size_t eakvd_v_sum_work_bytes(const eakvd_geom *g, int seq_len,
 {
     if (seq_len <= 0) return 0;
     const int n_chunks = ceil_div_i(seq_len, kChunk);
-    const size_t valu = (size_t)n_chunks * n_q * g->head_dim * sizeof(float);
+    size_t valu = (size_t)n_chunks * n_q * g->head_dim * sizeof(float);
+    // the MHA program's partials (one q head per kv head: n_kv = n_q)
+    const size_t mha = (size_t)mha_plan(g->head_dim, seq_len, n_q).nc * n_q * g->head_dim *
+                       sizeof(float);
+    valu = valu > mha ? valu : mha;
     const size_t mfma = eakvd_v_sum_mfma_work_bytes(g, seq_len, n_q);
     return valu > mfma ? valu : mfma;
 }
@@ -379,16 +391,13 @@ extern "C" int eakvd_v_sum(const eakvd_geom *g, const uint8_t *base,
     const int qpk = n_q / n_kv;
     float *partial = (float *)work;
     if (qpk == 1) {
-        const int chunk = mha_chunk(g->head_dim, seq_len, n_kv);
-        const int nc = ceil_div_i(seq_len, chunk);
-        const dim3 grid((unsigned)nc, (unsigned)n_kv);
+        const MhaPlan mp = mha_plan(g->head_dim, seq_len, n_kv);
+        const dim3 grid((unsigned)mp.nc, (unsigned)n_kv);
         uint8_t *ctr = const_cast<uint8_t *>(base) + g->ctr_off;
-        if (g->head_dim == 64)
-            hipLaunchKernelGGL(v_sum_mha_kernel<64>, grid, dim3(256), 0, st, p.w, p.s, p.b,
-                               g->gph, seq_len, w, chunk, n_q, partial, out, ctr);
-        else
-            hipLaunchKernelGGL(v_sum_mha_kernel<128>, grid, dim3(256), 0, st, p.w, p.s, p.b,
-                               g->gph, seq_len, w, chunk, n_q, partial, out, ctr);
+        auto kern = g->head_dim == 64 ? (mp.kb == 8 ? v_sum_mha_kernel<64, 8> : v_sum_mha_kernel<64, 2>)
+                                      : (mp.kb == 8 ? v_sum_mha_kernel<128, 8> : v_sum_mha_kernel<128, 2>);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, p.w, p.s, p.b, g->gph, seq_len, w,
+                           mp.chunk, n_q, partial, out, ctr);
         return (int)hipGetLastError();
     }
     const int n_chunks = ceil_div_i(seq_len, kChunk);

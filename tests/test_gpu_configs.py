@@ -109,12 +109,16 @@ def unfused_check(g, o, q, layer, n_q, n_kv, rng, signed=True):
     ("32q8kv-d128-32768", 1, 8, 32, 128, 32768, 0),
     ("mha-d64-1500", 1, 4, 4, 64, 1500, 0),
     ("mha-d128-5000", 2, 2, 2, 128, 5000, 1),
+    ("mha-d128-40000", 1, 2, 2, 128, 40000, 0),
+    ("mha-d64-70000", 1, 2, 2, 64, 70000, 0),
 ])
 def test_unfused_at_workload_shapes(E, rng, name, nl, nh, n_q, d, L, layer):
     """The reference API's unfused step at the benchmark shapes.  The MHA
-    V-sums sum 8 (2048 tokens), 32 (8192), 6 (d64 1500) and 20 (5000)
-    256-token chunks, so the chunk partials and their fixed-order sum are
-    all exercised."""
+    V-sums cover 512-token chunks at d128 and 1024-token chunks at d64: 4
+    (2048 tokens), 16 (8192), 2 (d64 1500), 10 (5000), 79 (40000) and 69
+    (d64 70000) chunk partials, added by the last block of each kv head in
+    batches of 16, so the partials, the counters and the fixed-order sum are
+    all exercised, on every call of unfused_check again."""
     say("unfused", name)
     data = (rng.standard_normal(nl * 2 * nh * L * d) * 1.5).astype(np.float32)
     g, o = pair(E, nl, nh, d, L)
