@@ -485,18 +485,18 @@ def fused_call_us(w, steps, warmup):
     return timed(H, w.stream, run, steps, warmup, c["nl"])
 
 
-def read_peak(n_bytes, regions=8, reps=3):
+def read_peak(n_bytes, regions=8, reps=3, per_cu=3):
     """Sustained HBM read rate of the synth library's plain streaming read
     kernel over passes of n_bytes: `regions` separate buffers read back to
     back (no pass finds its bytes in the last-level cache), best of `reps`
-    rounds; 3 blocks of 256 threads per CU.  Returns GB/s."""
+    rounds; per_cu blocks of 256 threads per CU.  Returns GB/s."""
     from eakv_amd import hipmem as H
     lib = Synth().lib
     lib.eakv_synth_read.restype = C.c_int
     lib.eakv_synth_read.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_void_p]
     n_bytes = (n_bytes + 15) // 16 * 16
     lib.eakv_synth_cu_count.restype = C.c_int
-    blocks = 3 * (lib.eakv_synth_cu_count() or 256)
+    blocks = per_cu * (lib.eakv_synth_cu_count() or 256)
     buf = H.DeviceArray((regions * n_bytes // 4,))
     buf.zero()
     H.synchronize()
@@ -516,6 +516,24 @@ def read_peak(n_bytes, regions=8, reps=3):
     buf.free()
     sink.free()
     return n_bytes / best / 1e6
+
+
+def floors_bench():
+    """The floors a dependent launch sits on: µs per launch of the plain
+    streaming read, 32 launches back to back on one stream over separate
+    buffers, for pass sizes from one 16-byte load (the launch cost alone) to
+    the fused call's, at 2, 3 and 4 blocks of 256 threads per CU."""
+    sizes = [16, 22_036_480, 41_975_808, 83_951_616, 167_837_696, 335_806_464]
+    res = []
+    for n in sizes:
+        row = {"bytes": n}
+        for per_cu in (2, 3, 4):
+            g = read_peak(n, regions=32, reps=4, per_cu=per_cu)
+            row[f"us_per_launch_{per_cu}_per_cu"] = round(((n + 15) // 16 * 16) / g / 1e3, 2)
+        res.append(row)
+    return {"metric": "back-to-back plain streaming read, µs per launch", "unit": "us",
+            "n_gpus": 1, "note": "32 separate buffers per round, best of 4 rounds; 16 bytes "
+            "measures the cost of a dependent launch itself", "floors": res}
 
 
 def gbs(nbytes, us):
@@ -668,6 +686,9 @@ def main():
     ap.add_argument("--ggml", action="store_true",
                     help="only time the ggml block type's device functions on 1 GiB of "
                          "f32 rows, print their JSON line, then exit")
+    ap.add_argument("--floors", action="store_true",
+                    help="only time back-to-back plain reads of the workloads' pass sizes "
+                         "(the launch and read floors), print their JSON line, then exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB, 5 times (the "
                          "known-size kernel for HBM byte counters), then exit")
@@ -681,6 +702,9 @@ def main():
         return
     if args.ggml:
         print(json.dumps(ggml_bench(max(1, args.steps), 2)), flush=True)
+        return
+    if args.floors:
+        print(json.dumps(floors_bench()), flush=True)
         return
     log = lambda *a: print(*a, file=sys.stderr, flush=True)
     if args.dequant or args.validate or args.unfused:
