@@ -160,7 +160,8 @@ static int fused_launch(eakv_cache_t *const *caches, int n, int layer,
     }
     const size_t need = eakvd_fused_work_bytes(&c0->geom, &b, n_q);
     return eakvd_fused(&c0->geom, &b, layer, d_q, n_q, n_kv, d_out,
-                       (char *)c0->work + (c0->work_bytes - need), stream);
+                       (char *)c0->work + (c0->work_bytes - need),
+                       c0->dev + c0->geom.ctr_off, stream);
 }
 
 int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
@@ -296,7 +297,8 @@ int eakv_attention_fused_batch_device_noalloc(eakv_cache_t *const *caches,
         if (e) rc = eakvi_hip_fail(e, "fused_noalloc: scratch address");
     }
     if (rc == EAKV_OK) {
-        int e = eakvd_fused(&c0->geom, &b, layer, d_q, n_q, n_kv, d_out, scr, st);
+        /* no counters: the static scratch is shared by every caller */
+        int e = eakvd_fused(&c0->geom, &b, layer, d_q, n_q, n_kv, d_out, scr, NULL, st);
         if (e) rc = eakvi_hip_fail(e, "fused_noalloc launch");
     }
     eakvi_leave(prev);

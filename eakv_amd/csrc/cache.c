@@ -59,7 +59,8 @@ void eakvd_geom_init(eakvd_geom *g, int n_layers, int n_kv_heads,
     g->b_off = g->s_off + round256(g->max_groups * 4);
     g->block_bytes = g->b_off + round256(g->max_groups * 4);
     g->ctr_off = g->block_bytes * 2 * n_layers + EAKVD_TAIL_PAD;
-    g->dev_bytes = g->ctr_off + (int64_t)n_kv_heads * EAKVD_CTR_STRIDE;
+    g->ctr_slots = n_kv_heads > EAKVD_CTR_MIN_SLOTS ? n_kv_heads : EAKVD_CTR_MIN_SLOTS;
+    g->dev_bytes = g->ctr_off + g->ctr_slots * EAKVD_CTR_STRIDE;
 }
 
 int eakvi_enter(const eakv_cache_t *c, int *prev)

@@ -9,9 +9,9 @@
  *   group index inside a plane = h*gph + t*gpd + j  (gph = max_seq_len*gpd,
  *   gpd = head_dim/64), the indexing of reference src/cache.c:69,:137 and
  *   src/attention.c:7.  Block and plane starts are rounded up to 256 bytes.
- *   After the last block: EAKVD_TAIL_PAD bytes, then at ctr_off one chunk
- *   counter per kv head, EAKVD_CTR_STRIDE bytes apart (the unfused V-sum's;
- *   zero between calls).
+ *   After the last block: EAKVD_TAIL_PAD bytes, then at ctr_off ctr_slots
+ *   chunk counters, EAKVD_CTR_STRIDE bytes apart, zero between calls (the
+ *   launches that merge their chunks themselves count on them).
  */
 #ifndef EAKVD_H
 #define EAKVD_H
@@ -34,6 +34,10 @@ extern "C" {
 /* Bytes between two chunk counters: counters on separate 64-byte lines do
  * not serialize one another's atomics. */
 #define EAKVD_CTR_STRIDE 64
+/* Counters of a cache: one per kv head, and at least one per CU of the
+ * device (a launch merges its chunks itself only when its grid is smaller
+ * than the device, so its units fit). */
+#define EAKVD_CTR_MIN_SLOTS 256
 
 typedef struct {
     int     n_layers, n_kv_heads, head_dim, max_seq_len;
@@ -43,6 +47,7 @@ typedef struct {
     int64_t s_off, b_off; /* plane offsets inside a block, bytes */
     int64_t block_bytes;  /* bytes per (layer, kv) block */
     int64_t ctr_off;      /* chunk counters, after the blocks and the tail pad */
+    int64_t ctr_slots;    /* how many */
     int64_t dev_bytes;    /* the whole device allocation */
 } eakvd_geom;
 
@@ -126,10 +131,13 @@ typedef struct {
 size_t eakvd_fused_work_bytes(const eakvd_geom *g, const eakvd_batch *b,
                               int n_q);
 /* work: eakvd_fused_work_bytes() of device scratch for the per-chunk
- * partial results; launches that share it must not overlap. */
+ * partial results; launches that share it must not overlap.  ctr: the
+ * counter region (g->ctr_slots counters at g->ctr_off of the cache whose
+ * workspace is used, zero between calls), or NULL: the chunks are then
+ * always merged by a second launch. */
 int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
                 const float *q, int n_q, int n_kv, float *out, void *work,
-                void *stream);
+                void *ctr, void *stream);
 /* The bytes of partials that eakvd_fused writes and reads for this batch
  * and head split (at most eakvd_fused_work_bytes()). */
 size_t eakvd_fused_launch_bytes(const eakvd_geom *g, const eakvd_batch *b,

@@ -47,6 +47,19 @@ __device__ __forceinline__ float ubyte_f32(uint32_t x)
     return r;
 }
 
+// Chunk partials cross blocks through device-scope (sc1) stores and loads: they
+// write through to, and read from, the device's coherence point, so no L2
+// writeback or invalidate (a whole-cache operation per XCD, costlier than
+// the kernel when every block pays it) is needed between blocks.
+__device__ __forceinline__ void st_dev(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p)
+{
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Reference reduce_add over 16 lanes, pairwise halving tree (the order the
 // CPU restatement fixes): v8[i]=a[i]+a[i+8], v4, v2, then v2[0]+v2[1].
 __device__ __forceinline__ float reduce16(const float *a)
@@ -77,6 +90,20 @@ __device__ __forceinline__ float wave_sum(float v)
 }
 
 static inline int ceil_div_i(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// Compute units of the current device (looked up once; 256 if unknown).
+static inline int cu_count()
+{
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0, v = 0;
+        n_cu = hipGetDevice(&dev) == hipSuccess &&
+                       hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                           hipSuccess && v > 0
+                   ? v : 256;
+    }
+    return n_cu;
+}
 
 // ---- Q4 group quantization pieces shared by the cache quantizer and the
 // ggml block type (16 lanes per 64-value group, lane l holding elements

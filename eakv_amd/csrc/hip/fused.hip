@@ -32,7 +32,8 @@
 //     byte column per lane) by ds_read_b64_tr_b8; the digits of a are
 //     exchanged through LDS the same way.  sum p*bias per (head, group) is
 //     kept apart and added at the end.
-//   Waves are merged in LDS, chunks by merge_kernel.
+//   Waves are merged in LDS, chunks by merge_kernel (or, for a grid smaller
+//   than the device, by the last block of each unit in the same launch).
 // valu_kernel (caches whose (layer, kv) blocks are beyond the 32-bit buffer
 //   offsets of mfma_kernel, above 1 GiB; every group size has a split into
 //   virtual kv heads, at worst of one q head each): one lane per token for K
@@ -394,6 +395,78 @@ struct WaveState {
     float lsum, m;
 };
 
+// The chunk merges of a launch that merges its own chunks (at most
+// kInBatch chunks per unit): the partials of one (sequence, q head) at p,
+// n_chunks of them, read with device-scope loads all issued at once (one
+// round trip).  Each thread restates, for its output i, the arithmetic of
+// the merge launch the same call would make, in the same order, so both
+// give the same bits: merge_kernel, and vsum_merge_kernel in V-sum mode.
+constexpr int kInBatch = 16;    // merge_kernel's batch
+constexpr int kInParts = 8;     // vsum_merge_kernel's parts
+
+// Softmax merge: M = max(-1e6 log2(e), m_c), l = sum l_c 2^(m_c - M),
+// o = sum o_c 2^(m_c - M), out = o * (1/l).
+template <int D>
+__device__ __forceinline__ float merge_chunks(const float *p, int n_chunks, int i)
+{
+    float m[kInBatch], lv[kInBatch], ov[kInBatch];
+#pragma unroll
+    for (int j = 0; j < kInBatch; j++) {
+        const float *pc = p + min(j, n_chunks - 1) * (D + 2);
+        m[j] = ld_dev(pc);
+        lv[j] = ld_dev(pc + 1);
+        ov[j] = ld_dev(pc + 2 + i);
+    }
+    const float M = -1000000.0f * EAKV_LOG2E;
+    float Mn = M, lt = 0.0f, ot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kInBatch; j++)
+        if (j < n_chunks) Mn = fmaxf(Mn, m[j]);
+    const float f = __builtin_amdgcn_exp2f(M - Mn);
+    lt *= f;
+    ot *= f;
+#pragma unroll
+    for (int j = 0; j < kInBatch; j++) {
+        const float wj = j < n_chunks ? __builtin_amdgcn_exp2f(m[j] - Mn) : 0.0f;
+        lt = fmaf(lv[j], wj, lt);
+        ot = fmaf(ov[j], wj, ot);
+    }
+    return ot * (1.0f / lt);
+}
+
+// V-sum mode: the plain sum of o_c in 8 strided parts (chunks pt, pt + 8)
+// added in part order, NaN when a chunk's l is NaN (a non-finite weight).
+template <int D>
+__device__ __forceinline__ float vs_chunk_sum(const float *p, int n_chunks, int i)
+{
+    float o[kInBatch], l[kInBatch];
+#pragma unroll
+    for (int j = 0; j < kInBatch; j++) {
+        const float *pc = p + min(j, n_chunks - 1) * (D + 2);
+        l[j] = ld_dev(pc + 1);
+        o[j] = ld_dev(pc + 2 + i);
+    }
+    float t = 0.0f, fl = 0.0f;
+#pragma unroll
+    for (int pt = 0; pt < kInParts; pt++) {
+        float sum = 0.0f, bad = 0.0f;
+#pragma unroll
+        for (int c = pt; c < kInBatch; c += kInParts)
+            if (c < n_chunks) {
+                sum = __fadd_rn(sum, o[c]);
+                bad = bad + l[c];                 // 0, or NaN after a non-finite weight
+            }
+        if (pt == 0) {
+            t = sum;
+            fl = bad;
+        } else {
+            t = __fadd_rn(t, sum);
+            fl = fl + bad;
+        }
+    }
+    return fl == fl ? t : fl;
+}
+
 // Tile assignment: nb = gridDim.x blocks share one (sequence, kv head), a
 // "unit" of n_tiles kTT-token tiles, dealt round robin: tile j to block
 // (j / kWaves) % nb and wave j % kWaves.  At any time the waves of a unit
@@ -417,7 +490,8 @@ struct WaveState {
 template <int D, int HH, bool VS>
 __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, HH> / 4)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
-    int n_q, int qpk, float rs, float *__restrict__ part, int split)
+    int n_q, int qpk, float rs, float *__restrict__ part, int split,
+    float *__restrict__ out, uint8_t *__restrict__ ctr)
 {
     constexpr int GPD = D / 64;
     constexpr int NK = Geo<D>::NK;
@@ -448,7 +522,17 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
     const int n_tiles = (L + kTT - 1) / kTT;
-    if (ch * NW >= n_tiles) return;         // no tile for this block: no partial
+    if (ch * NW >= n_tiles) {         // no tile for this block: no partial
+        // merged here, an empty sequence's outputs are 0 * (1/0) = NaN, as
+        // the reference's (and merge_kernel's)
+        if constexpr (!VS)
+            if (ctr && n_tiles == 0 && ch == 0) {
+                const float zl = 0.0f, zo = 0.0f;
+                for (int i = threadIdx.x; i < qpk * D; i += 64 * NW)
+                    out[((int64_t)s * n_q + (int64_t)kvh * qpk) * D + i] = zo * (1.0f / zl);
+            }
+        return;
+    }
     if constexpr (HH > 1) {
         if (threadIdx.x == 0) q_ctr = 0;
         __syncthreads();
@@ -1043,11 +1127,46 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             ot = fmaf(o[(h & 3) * D + dim], f, ot);
         }
         float *dst = part + (((int64_t)s * n_q + kvh * qpk + h) * nb + ch) * (D + 2);
-        dst[2 + dim] = ot;
-        if (dim == 0) {
-            dst[0] = M;
-            dst[1] = lt;
+        if (ctr) {
+            st_dev(dst + 2 + dim, ot);
+            if (dim == 0) {
+                st_dev(dst, M);
+                st_dev(dst + 1, lt);
+            }
+        } else {
+            dst[2 + dim] = ot;
+            if (dim == 0) {
+                dst[0] = M;
+                dst[1] = lt;
+            }
         }
+    }
+    if (!ctr) return;
+
+    // ---- the chunk merge in this launch (small grids): every thread's
+    // partial stores are complete (vmcnt 0) before the barrier, and so
+    // before the block counts itself on its unit's counter; the block that
+    // counts last reads the unit's partials after it, merges them into out
+    // and sets the counter back to zero (no other block of the launch
+    // touches it again)
+    const int n_chunks = min(nb, (n_tiles + NW - 1) / NW);   // blocks with a tile
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned *uc = reinterpret_cast<unsigned *>(
+        ctr + ((int64_t)s * gridDim.y + kvh) * EAKVD_CTR_STRIDE);
+    if (tid == 0)
+        ((int *)z_lds[0])[0] = __hip_atomic_fetch_add(uc, 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT) ==
+                               (unsigned)(n_chunks - 1);
+    __syncthreads();
+    if (((const int *)z_lds[0])[0] == 0) return;
+    if (tid == 0) __hip_atomic_store(uc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = tid; i < G * D; i += 64 * NW) {
+        const int h = i / D, dim = i % D;
+        const int64_t qh = (int64_t)s * n_q + kvh * qpk + h;
+        const float *pq = part + qh * nb * (D + 2);
+        out[qh * D + dim] = VS ? vs_chunk_sum<D>(pq, n_chunks, dim)
+                               : merge_chunks<D>(pq, n_chunks, dim);
     }
 }
 
@@ -1415,16 +1534,7 @@ __global__ __launch_bounds__(D) void combine_kernel(
 // 32Q/32KV at 8192 15.0 -> 17.5 us with them everywhere.
 int mfma_blocks_per_unit(int ml, int units, int per_cu)
 {
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
-                hipSuccess && v > 0)
-            n_cu = v;
-        else
-            n_cu = 256;
-    }
+    const int n_cu = cu_count();
     const int slots = n_cu * per_cu;
     int nb = units >= slots ? 1 : slots / units;
     const int coarse = (ml + 2 * kChunkM - 1) / (2 * kChunkM);
@@ -1521,9 +1631,21 @@ extern "C" int eakvd_scratch(void **p)
     return 0;
 }
 
+// The chunks merged in the main launch: where counters are given, the grid
+// is smaller than the device (the merge launch would be most of such a call;
+// on large grids the merging blocks' tail costs more than the launch) and a
+// unit has at most kInBatch chunks (one round trip of loads).
+bool merge_in_launch(const eakvd_geom *g, const void *ctr, int mc, int64_t units)
+{
+#ifdef EAKV_NO_MERGE_IN_LAUNCH
+    return false;
+#endif
+    return ctr && units * mc < cu_count() && mc <= kInBatch && units <= g->ctr_slots;
+}
+
 extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
                            int layer, const float *q, int n_q, int n_kv,
-                           float *out, void *work, void *stream)
+                           float *out, void *work, void *ctr, void *stream)
 {
     const hipStream_t st = (hipStream_t)stream;
     const float rs = 1.0f / sqrtf((float)g->head_dim);
@@ -1539,8 +1661,11 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         auto kern = g->head_dim == 64
                         ? (hh == 1 ? mfma_kernel<64, 1, false> : mfma_kernel<64, 2, false>)
                         : (hh == 1 ? mfma_kernel<128, 1, false> : mfma_kernel<128, 2, false>);
+        const int64_t units = (int64_t)n_kv * p.split * b->n_seq;
+        uint8_t *uc = merge_in_launch(g, ctr, mc, units) ? (uint8_t *)ctr : nullptr;
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, p.qv, rs,
-                           part, p.split);
+                           part, p.split, out, uc);
+        if (uc) return (int)hipGetLastError();
         if (parts && g->head_dim == 64)
             hipLaunchKernelGGL(merge_parts_kernel<64>, pgrid, dim3(256), 0, st, *b, n_q, mc,
                                wpb, part, out);
@@ -1616,8 +1741,12 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
     auto kern = g->head_dim == 64
                     ? (hh == 1 ? mfma_kernel<64, 1, true> : mfma_kernel<64, 2, true>)
                     : (hh == 1 ? mfma_kernel<128, 1, true> : mfma_kernel<128, 2, true>);
+    const int64_t units = (int64_t)n_kv * split;
+    uint8_t *ctr = const_cast<uint8_t *>(base) + g->ctr_off;
+    uint8_t *uc = merge_in_launch(g, ctr, mc, units) ? ctr : nullptr;
     hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, b, layer, w, n_q, qv, 0.0f,
-                       part, split);
+                       part, split, out, uc);
+    if (uc) return (int)hipGetLastError();
     // the chunks that hold a partial: blocks with a tile (see mfma_kernel)
     const int n_tiles = (seq_len + kTT - 1) / kTT;
     const int nch = min(mc, (n_tiles + wpb - 1) / wpb);

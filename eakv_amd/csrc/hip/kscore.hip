@@ -220,14 +220,7 @@ void k_score_mha_kernel(
 // 256-token slice.
 int k_blocks(int n_sl, int n_kv)
 {
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0, v = 0;
-        n_cu = hipGetDevice(&dev) == hipSuccess &&
-                       hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
-                           hipSuccess && v > 0
-                   ? v : 256;
-    }
+    const int n_cu = cu_count();
     const int want = (kKsBlocksPerCU * n_cu + n_kv - 1) / n_kv;
     return want < n_sl ? want : n_sl;
 }

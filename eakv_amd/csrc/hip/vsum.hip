@@ -48,19 +48,6 @@ struct MhaGeo {
     static constexpr int STEP = TS * KB;           // tokens per batch of a block
 };
 
-// Partials cross blocks through device-scope (sc1) stores and loads: they
-// write through to, and read from, the device's coherence point, so no L2
-// writeback or invalidate (a whole-cache operation per XCD, costlier than
-// the kernel when every block pays it) is needed between blocks.
-__device__ __forceinline__ void st_dev(float *p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float *p)
-{
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Block (ch, kvh): tokens [ch*chunk, min(L, ch*chunk + chunk)) of kv head kvh
 // (= q head kvh), weights w[kvh][t].  With one chunk the block writes
 // out[kvh][D]; otherwise it writes partial[ch][kvh][D], counts itself on the
@@ -335,14 +322,7 @@ struct MhaPlan {
 
 MhaPlan mha_plan(int D, int L, int n_kv)
 {
-    static int n_cu = 0;
-    if (n_cu == 0) {
-        int dev = 0, v = 0;
-        n_cu = hipGetDevice(&dev) == hipSuccess &&
-                       hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
-                           hipSuccess && v > 0
-                   ? v : 256;
-    }
+    const int n_cu = cu_count();
     const int ts = D == 64 ? MhaGeo<64, 8>::TS : MhaGeo<128, 8>::TS;
     MhaPlan p;
     p.kb = (int64_t)n_kv * ceil_div_i(L, ts * 8) >= n_cu ? 8 : 2;
