@@ -401,15 +401,18 @@ def test_fused_batch_device(E, rng):
         assert ok, (lens[i], err, nbad)
 
 
-@pytest.mark.parametrize("d", [64, 128])
-def test_fused_batch_long_short_and_empty(E, rng, d):
-    """A batch whose longest sequence splits into more than 16 chunks (the
-    8-part chunk merge) beside short sequences with fewer chunks and an empty
-    one: each sequence merges only its own chunks, and the empty one gives
-    NaN, as the reference's 0 * (1/0)."""
+@pytest.mark.parametrize("d,lens,lmax", [
+    (64, [0, 5, 4600, 300], 4608), (128, [0, 5, 4600, 300], 4608),
+    (64, [0, 5, 1000, 300], 1024), (128, [300, 0, 1000, 1], 1024)])
+def test_fused_batch_long_short_and_empty(E, rng, d, lens, lmax):
+    """A batch of long, short and empty sequences.  With 4600 tokens the
+    longest splits into more than 16 chunks (the 8-part merge launch); with
+    1000 the grid is smaller than the device and the launch merges its own
+    chunks (counters in the first cache).  Each sequence merges only its own
+    chunks, the empty one gives NaN, as the reference's 0 * (1/0), and a
+    second call (the counters back at zero) gives the same bits."""
     from eakv_amd.hipmem import DeviceArray
-    nl, nh, n_q, lmax = 1, 2, 8, 4608
-    lens = [0, 5, 4600, 300]
+    nl, nh, n_q = 1, 2, 8
     gs, os_ = [], []
     for L in lens:
         g, o = pair(E, nl, nh, d, lmax) if L == 0 else loaded(E, rng, nh, d, L, lmax, nl)
@@ -422,10 +425,20 @@ def test_fused_batch_long_short_and_empty(E, rng, d):
                                                      n_q, nh, dout.ptr, None) == 0
     gs[0].sync()
     out = dout.download()
-    assert np.isnan(out[0]).all()
-    for i in range(1, len(lens)):
+    for i, L in enumerate(lens):
+        if L == 0:
+            assert np.isnan(out[i]).all()
+            continue
         ok, err, nbad = tol_close(out[i], os_[i].attention_fused(q[i], 0, n_q, nh), ATOL, RTOL)
-        assert ok, (lens[i], err, nbad)
+        assert ok, (L, err, nbad)
+    from eakv_amd.hipmem import synchronize
+    dout.zero()
+    synchronize()
+    assert E.lib().eakv_attention_fused_batch_device(E.handles(gs), len(gs), 0, dq.ptr,
+                                                     n_q, nh, dout.ptr, None) == 0
+    gs[0].sync()
+    again = dout.download()
+    assert np.array_equal(again.view(np.uint32), out.view(np.uint32))
 
 
 def test_workspace_ordered_across_caller_streams(E, rng):
