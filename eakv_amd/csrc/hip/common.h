@@ -105,9 +105,10 @@ static inline int cu_count()
     return n_cu;
 }
 
-// ---- Q4 group quantization pieces shared by the cache quantizer and the
-// ggml block type (16 lanes per 64-value group, lane l holding elements
-// 4l..4l+3 as a float4; slot_shift = the group's first lane in the wave).
+// ---- Q4 group quantization pieces shared by the cache quantizer (q4) and
+// the ggml block type (all of them: 16 lanes per 64-value group, lane l
+// holding elements 4l..4l+3 as a float4; slot_shift = the group's first
+// lane in the wave).
 
 // f32 -> i32 with x86 cvttss2si semantics (NaN / out of range -> INT32_MIN).
 __device__ __forceinline__ int to_i32_x86(float v)

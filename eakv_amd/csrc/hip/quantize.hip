@@ -12,22 +12,119 @@
 //            INT32_MIN, then clamped to 0)
 //   byte k = q(x[k+32])*16 + q(x[k])
 //
-// Work split: 16 lanes per group, each lane one float4 (elements 4l..4l+3,
-// so lanes 0-7 carry the low-nibble half and lanes 8-15 the high half).
-// A wave covers 4 groups = 1 KB of contiguous f32 per load instruction.
+// Work split: 8 lanes per group; lane j holds elements 4j..4j+3 (its four
+// low nibbles) and 32+4j..32+4j+3 (their high nibbles), so it packs its own
+// four bytes.  A wave covers 8 groups (2 KB of f32) with two 16-byte loads
+// per lane; each lane loads its next group before it quantizes the current
+// one.  The group min and max combine across the 8 lanes by DPP moves.
 #include "common.h"
 
 namespace {
 
-template <int NT, bool VEC>
-__global__ __launch_bounds__(NT) void quantize_kernel(eakvd_geom g,
-                                                      eakvd_quant_job job)
+#ifndef EAKV_QUANT_BLOCKS
+#define EAKV_QUANT_BLOCKS 8192
+#endif
+constexpr int64_t kQuantBlocks = EAKV_QUANT_BLOCKS;
+constexpr int64_t kOnePass = 32768;
+
+// DPP moves within 8-lane groups: the mirror of each half row (lane i and
+// 7 - i), and the quad permutations xor 2 and xor 1.
+constexpr int kDppHalfMirror = 0x141, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
 {
-    const int lane16 = threadIdx.x & 15;
-    const int slot = threadIdx.x >> 4;
-    const int slot_shift = (threadIdx.x & 63) & ~15;
-    const int64_t slots = NT / 16;
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// The first element of the group, in index order, that compares equal to
+// zero (the group has one): the low halves of lanes 0-7 hold elements 0-31,
+// the high halves 32-63.  gbase: the group's first lane in the wave.
+__device__ __forceinline__ float first_zero8(const float4 &lo, const float4 &hi, int gbase)
+{
+    const float zl = lo.x == 0.0f ? lo.x : (lo.y == 0.0f ? lo.y : (lo.z == 0.0f ? lo.z : lo.w));
+    const float zh = hi.x == 0.0f ? hi.x : (hi.y == 0.0f ? hi.y : (hi.z == 0.0f ? hi.z : hi.w));
+    const bool hl = (lo.x == 0.0f) | (lo.y == 0.0f) | (lo.z == 0.0f) | (lo.w == 0.0f);
+    const bool hh = (hi.x == 0.0f) | (hi.y == 0.0f) | (hi.z == 0.0f) | (hi.w == 0.0f);
+    const uint32_t bl = (uint32_t)(__ballot(hl) >> gbase) & 0xffu;
+    const uint32_t bh = (uint32_t)(__ballot(hh) >> gbase) & 0xffu;
+    const int sl = bl ? __ffs((int)bl) - 1 : 0;
+    const int sh = bh ? __ffs((int)bh) - 1 : 0;
+    const float vl = __shfl(zl, sl, 8), vh = __shfl(zh, sh, 8);
+    return bl ? vl : vh;
+}
+
+// One group: the reference's min/max, scale, bias and nibbles; lane j's
+// four packed bytes, and (lane 0) the scale and bias.
+struct QOut {
+    uint32_t word;
+    float scale, bias;
+};
+
+__device__ __forceinline__ QOut quantize_group8(const float4 &lo, const float4 &hi, int gbase)
+{
+    float mn = fminf(fminf(fminf(lo.x, lo.y), fminf(lo.z, lo.w)),
+                     fminf(fminf(hi.x, hi.y), fminf(hi.z, hi.w)));
+    float mx = fmaxf(fmaxf(fmaxf(lo.x, lo.y), fmaxf(lo.z, lo.w)),
+                     fmaxf(fmaxf(hi.x, hi.y), fmaxf(hi.z, hi.w)));
+    mn = fminf(mn, dpp_f<kDppHalfMirror>(mn));
+    mx = fmaxf(mx, dpp_f<kDppHalfMirror>(mx));
+    mn = fminf(mn, dpp_f<kDppXor2>(mn));
+    mx = fmaxf(mx, dpp_f<kDppXor2>(mx));
+    mn = fminf(mn, dpp_f<kDppXor1>(mn));
+    mx = fmaxf(mx, dpp_f<kDppXor1>(mx));
+    // a zero min or max: the first zero's sign, as a strict scan keeps it
+    if (mn == 0.0f || mx == 0.0f) {
+        const float z = first_zero8(lo, hi, gbase);
+        if (mn == 0.0f) mn = z;
+        if (mx == 0.0f) mx = z;
+    }
+    // a NaN element 0 makes min = max = that NaN
+    if (__ballot((threadIdx.x & 7) == 0 && lo.x != lo.x) != 0) {
+        const float x0 = __shfl(lo.x, 0, 8);
+        if (x0 != x0) {
+            mn = x0;
+            mx = x0;
+        }
+    }
+    const float range = __fsub_rn(mx, mn);
+    QOut o;
+    o.scale = 1.0f;
+    o.bias = mn;
+    float inv = 0.0f;
+    if (range > 0.0f) {
+        o.scale = range / 15.0f;
+        inv = 15.0f / range;
+    }
+    const uint32_t b0 = q4(lo.x, mn, inv) | (q4(hi.x, mn, inv) << 4);
+    const uint32_t b1 = q4(lo.y, mn, inv) | (q4(hi.y, mn, inv) << 4);
+    const uint32_t b2 = q4(lo.z, mn, inv) | (q4(hi.z, mn, inv) << 4);
+    const uint32_t b3 = q4(lo.w, mn, inv) | (q4(hi.w, mn, inv) << 4);
+    o.word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    return o;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_group8(const float *gp, int l8, float4 &lo, float4 &hi)
+{
+    const float *a = gp + l8 * 4, *b = gp + 32 + l8 * 4;
+    if (VEC) {
+        lo = *reinterpret_cast<const float4 *>(a);
+        hi = *reinterpret_cast<const float4 *>(b);
+    } else {
+        lo = make_float4(a[0], a[1], a[2], a[3]);
+        hi = make_float4(b[0], b[1], b[2], b[3]);
+    }
+}
+
+template <int NT, bool VEC>
+__global__ __launch_bounds__(NT) void quantize8_kernel(eakvd_geom g, eakvd_quant_job job)
+{
+    const int l8 = threadIdx.x & 7;
+    const int slot = threadIdx.x >> 3;
+    const int gbase = (threadIdx.x & 63) & ~7;
+    const int64_t slots = NT / 8;
     const int64_t per_cache = (int64_t)job.n_planes * job.nh;
+    const int64_t gstep = (int64_t)gridDim.x * slots;
 
     for (int64_t row = blockIdx.y; row < job.n_rows; row += gridDim.y) {
         const int c = (int)(row / per_cache);
@@ -35,46 +132,30 @@ __global__ __launch_bounds__(NT) void quantize_kernel(eakvd_geom g,
         const int plane = job.plane0 + (int)(rem / job.nh);
         const int64_t h = rem % job.nh;
         uint8_t *blk = job.base[c] + (int64_t)plane * g.block_bytes;
-        uint8_t *wp = blk;
         float *sp = (float *)(blk + g.s_off);
         float *bp = (float *)(blk + g.b_off);
         const int64_t gdst0 = h * g.gph + job.g_off[c];
         const float *srow = job.src + row * job.row_stride;
 
-        for (int64_t gi = (int64_t)blockIdx.x * slots + slot; gi < job.n_g;
-             gi += (int64_t)gridDim.x * slots) {
-            const float *xp = srow + gi * 64 + lane16 * 4;
-            float4 x;
-            if (VEC) {
-                x = *reinterpret_cast<const float4 *>(xp);
-            } else {
-                x.x = xp[0]; x.y = xp[1]; x.z = xp[2]; x.w = xp[3];
-            }
-
-            float mn, mx;
-            group_minmax(x, slot_shift, mn, mx);
-
-            const float range = __fsub_rn(mx, mn);
-            float scale = 1.0f, inv = 0.0f;
-            if (range > 0.0f) {
-                scale = range / 15.0f;
-                inv = 15.0f / range;
-            }
-
-            const uint32_t q0 = q4(x.x, mn, inv), q1 = q4(x.y, mn, inv);
-            const uint32_t q2 = q4(x.z, mn, inv), q3 = q4(x.w, mn, inv);
-            const uint32_t mine = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
-            const uint32_t hi = (uint32_t)__shfl_xor((int)mine, 8, 16);
-
+        // the 8 lanes of a group share its trip count, so the DPP moves and
+        // shuffles above only ever read lanes of the same group
+        int64_t gi = (int64_t)blockIdx.x * slots + slot;
+        float4 lo, hi;
+        if (gi < job.n_g) load_group8<VEC>(srow + gi * 64, l8, lo, hi);
+        while (gi < job.n_g) {
+            const int64_t gn = gi + gstep;
+            float4 nlo = lo, nhi = hi;
+            if (gn < job.n_g) load_group8<VEC>(srow + gn * 64, l8, nlo, nhi);
+            const QOut o = quantize_group8(lo, hi, gbase);
             const int64_t gd = gdst0 + gi;
-            if (lane16 < 8) {
-                *reinterpret_cast<uint32_t *>(wp + gd * 32 + lane16 * 4) =
-                    mine | (hi << 4);
+            *reinterpret_cast<uint32_t *>(blk + gd * 32 + l8 * 4) = o.word;
+            if (l8 == 0) {
+                sp[gd] = o.scale;
+                bp[gd] = o.bias;
             }
-            if (lane16 == 0) {
-                sp[gd] = scale;
-                bp[gd] = mn;
-            }
+            gi = gn;
+            lo = nlo;
+            hi = nhi;
         }
     }
 }
@@ -89,27 +170,27 @@ extern "C" int eakvd_quantize(const eakvd_geom *g, const eakvd_quant_job *job,
     const int64_t gy = job->n_rows < 65535 ? job->n_rows : 65535;
     // float4 loads need 16-byte aligned rows
     const bool vec = ((uintptr_t)job->src % 16 == 0) && (job->row_stride % 4 == 0);
-    if (job->n_g <= 4) {
+    if (job->n_g <= 8) {
+        // a token or two per row (appends): one block of 64 lanes per row
         const dim3 grid(1, (unsigned)gy);
         if (vec)
-            hipLaunchKernelGGL((quantize_kernel<64, true>), grid, dim3(64), 0,
-                               st, *g, *job);
+            hipLaunchKernelGGL((quantize8_kernel<64, true>), grid, dim3(64), 0, st, *g, *job);
         else
-            hipLaunchKernelGGL((quantize_kernel<64, false>), grid, dim3(64), 0,
-                               st, *g, *job);
+            hipLaunchKernelGGL((quantize8_kernel<64, false>), grid, dim3(64), 0, st, *g, *job);
     } else {
-        // about 8 K blocks of 16 groups per pass over the rows
-        int64_t need = (job->n_g + 15) / 16;
-        int64_t gx = (8192 + gy - 1) / gy;
+        // blocks of 32 groups: one pass over the rows where that takes at
+        // least kOnePass blocks (long rows), else about kQuantBlocks blocks
+        // (a few passes each)
+        const int64_t need = (job->n_g + 31) / 32;
+        const int64_t target = need * gy >= kOnePass ? need * gy : kQuantBlocks;
+        int64_t gx = (target + gy - 1) / gy;
         if (gx > need) gx = need;
         if (gx < 1) gx = 1;
         const dim3 grid((unsigned)gx, (unsigned)gy);
         if (vec)
-            hipLaunchKernelGGL((quantize_kernel<256, true>), grid, dim3(256), 0,
-                               st, *g, *job);
+            hipLaunchKernelGGL((quantize8_kernel<256, true>), grid, dim3(256), 0, st, *g, *job);
         else
-            hipLaunchKernelGGL((quantize_kernel<256, false>), grid, dim3(256), 0,
-                               st, *g, *job);
+            hipLaunchKernelGGL((quantize8_kernel<256, false>), grid, dim3(256), 0, st, *g, *job);
     }
     return (int)hipGetLastError();
 }
