@@ -105,10 +105,8 @@ static inline int cu_count()
     return n_cu;
 }
 
-// ---- Q4 group quantization pieces shared by the cache quantizer (q4) and
-// the ggml block type (all of them: 16 lanes per 64-value group, lane l
-// holding elements 4l..4l+3 as a float4; slot_shift = the group's first
-// lane in the wave).
+// ---- Q4 group quantization pieces shared by the cache quantizer and the
+// ggml block type (8 lanes per 64-value group).
 
 // f32 -> i32 with x86 cvttss2si semantics (NaN / out of range -> INT32_MIN).
 __device__ __forceinline__ int to_i32_x86(float v)
@@ -125,40 +123,66 @@ __device__ __forceinline__ uint32_t q4(float x, float mn, float inv)
     return (uint32_t)q;
 }
 
-// First element (in index order 4*lane16 + i) of the group that compares
-// equal to zero; its value carries the sign a strict scan keeps.
-__device__ __forceinline__ float first_zero(const float4 &x, int slot_shift)
+// DPP moves within 8-lane groups: the mirror of each half row (lane i and
+// 7 - i), and the quad permutations xor 2 and xor 1.
+constexpr int kDppHalfMirror = 0x141, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
 {
-    float mine = x.x == 0.0f ? x.x
-               : (x.y == 0.0f ? x.y : (x.z == 0.0f ? x.z : x.w));
-    bool has = (x.x == 0.0f) | (x.y == 0.0f) | (x.z == 0.0f) | (x.w == 0.0f);
-    uint64_t m = __ballot(has);
-    uint32_t sm = (uint32_t)(m >> slot_shift) & 0xffffu;
-    int src = __ffs((int)sm) - 1;
-    if (src < 0) src = 0;
-    return __shfl(mine, src, 16);
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 
-// min and max of a group as a strict </> scan from element 0 finds them:
-// the first occurrence wins (so +0 / -0 as they come first), NaN elements
-// after element 0 are skipped, a NaN element 0 gives min = max = NaN.
-__device__ __forceinline__ void group_minmax(const float4 &x, int slot_shift, float &mn,
-                                             float &mx)
+// The first element of the group, in index order, that compares equal to
+// zero (the group has one): the low halves of lanes 0-7 hold elements 0-31,
+// the high halves 32-63.  gbase: the group's first lane in the wave.
+__device__ __forceinline__ float first_zero8(const float4 &lo, const float4 &hi, int gbase)
 {
-    mn = fminf(fminf(x.x, x.y), fminf(x.z, x.w));
-    mx = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) {
-        mn = fminf(mn, __shfl_xor(mn, o, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, o, 16));
-    }
+    const float zl = lo.x == 0.0f ? lo.x : (lo.y == 0.0f ? lo.y : (lo.z == 0.0f ? lo.z : lo.w));
+    const float zh = hi.x == 0.0f ? hi.x : (hi.y == 0.0f ? hi.y : (hi.z == 0.0f ? hi.z : hi.w));
+    const bool hl = (lo.x == 0.0f) | (lo.y == 0.0f) | (lo.z == 0.0f) | (lo.w == 0.0f);
+    const bool hh = (hi.x == 0.0f) | (hi.y == 0.0f) | (hi.z == 0.0f) | (hi.w == 0.0f);
+    const uint32_t bl = (uint32_t)(__ballot(hl) >> gbase) & 0xffu;
+    const uint32_t bh = (uint32_t)(__ballot(hh) >> gbase) & 0xffu;
+    const int sl = bl ? __ffs((int)bl) - 1 : 0;
+    const int sh = bh ? __ffs((int)bh) - 1 : 0;
+    const float vl = __shfl(zl, sl, 8), vh = __shfl(zh, sh, 8);
+    return bl ? vl : vh;
+}
+
+// min and max of a 64-value group held by 8 lanes (lane j: elements 4j..4j+3
+// in lo, 32+4j..32+4j+3 in hi; gbase = the group's first lane in the wave)
+// as a strict </> scan from element 0 finds them: the first occurrence wins
+// (so +0 / -0 as they come first), NaN elements after element 0 are
+// skipped, a NaN element 0 gives min = max = NaN.  Every lane of the group
+// gets both; the groups of a wave must run the same branches together
+// (their lanes share a trip count).
+__device__ __forceinline__ void group_minmax8(const float4 &lo, const float4 &hi, int gbase,
+                                              float &mn, float &mx)
+{
+    mn = fminf(fminf(fminf(lo.x, lo.y), fminf(lo.z, lo.w)),
+               fminf(fminf(hi.x, hi.y), fminf(hi.z, hi.w)));
+    mx = fmaxf(fmaxf(fmaxf(lo.x, lo.y), fmaxf(lo.z, lo.w)),
+               fmaxf(fmaxf(hi.x, hi.y), fmaxf(hi.z, hi.w)));
+    mn = fminf(mn, dpp_f<kDppHalfMirror>(mn));
+    mx = fmaxf(mx, dpp_f<kDppHalfMirror>(mx));
+    mn = fminf(mn, dpp_f<kDppXor2>(mn));
+    mx = fmaxf(mx, dpp_f<kDppXor2>(mx));
+    mn = fminf(mn, dpp_f<kDppXor1>(mn));
+    mx = fmaxf(mx, dpp_f<kDppXor1>(mx));
+    // a zero min or max: the first zero's sign, as a strict scan keeps it
     if (mn == 0.0f || mx == 0.0f) {
-        const float z = first_zero(x, slot_shift);
+        const float z = first_zero8(lo, hi, gbase);
         if (mn == 0.0f) mn = z;
         if (mx == 0.0f) mx = z;
     }
-    const float x0 = __shfl(x.x, 0, 16);
-    if (x0 != x0) { mn = x0; mx = x0; }
+    // a NaN element 0 makes min = max = that NaN
+    if (__ballot((threadIdx.x & 7) == 0 && lo.x != lo.x) != 0) {
+        const float x0 = __shfl(lo.x, 0, 8);
+        if (x0 != x0) {
+            mn = x0;
+            mx = x0;
+        }
+    }
 }
 
 typedef int v4i __attribute__((ext_vector_type(4)));

@@ -8,39 +8,58 @@
 
 namespace {
 
-// Row to blocks, 16 lanes per block (lane l: elements 4l..4l+3).  min/max
-// as the strict scan of ggml_type.c:79-85; d = range/15 (0 for a constant
-// block), id = range > 0 ? 15/range : 0, q = clamp(trunc(0.5 + (x - min)*id),
-// 0, 15) (ggml_type.c:47-50, :79-87); byte k = q(x[k]) | q(x[k+32]) << 4.
+// Row to blocks, 8 lanes per block (lane j: elements 4j..4j+3 and
+// 32+4j..32+4j+3, so it packs its own four bytes).  min/max as the strict
+// scan of ggml_type.c:79-85; d = range/15 (0 for a constant block),
+// id = range > 0 ? 15/range : 0, q = clamp(trunc(0.5 + (x - min)*id), 0, 15)
+// (ggml_type.c:47-50, :79-87); byte k = q(x[k]) | q(x[k+32]) << 4.  Each
+// lane loads its next block before it quantizes the current one.
+template <bool VEC>
+__device__ __forceinline__ void load_block8(const float *bp, int l8, float4 &lo, float4 &hi)
+{
+    const float *a = bp + l8 * 4, *c = bp + 32 + l8 * 4;
+    if (VEC) {
+        lo = *reinterpret_cast<const float4 *>(a);
+        hi = *reinterpret_cast<const float4 *>(c);
+    } else {
+        lo = make_float4(a[0], a[1], a[2], a[3]);
+        hi = make_float4(c[0], c[1], c[2], c[3]);
+    }
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void ggml_quantize_kernel(const float *__restrict__ src,
                                                             uint8_t *__restrict__ dst, int64_t nb)
 {
-    const int lane16 = threadIdx.x & 15;
-    const int slot_shift = (threadIdx.x & 63) & ~15;
-    for (int64_t b = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4); b < nb;
-         b += (int64_t)gridDim.x * 16) {
-        const float *xp = src + b * 64 + lane16 * 4;
-        float4 x;
-        if (VEC) {
-            x = *reinterpret_cast<const float4 *>(xp);
-        } else {
-            x.x = xp[0]; x.y = xp[1]; x.z = xp[2]; x.w = xp[3];
-        }
+    const int l8 = threadIdx.x & 7;
+    const int gbase = (threadIdx.x & 63) & ~7;
+    const int64_t step = (int64_t)gridDim.x * 32;
+    // the 8 lanes of a block share its trip count
+    int64_t b = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    float4 lo, hi;
+    if (b < nb) load_block8<VEC>(src + b * 64, l8, lo, hi);
+    while (b < nb) {
+        const int64_t bn = b + step;
+        float4 nlo = lo, nhi = hi;
+        if (bn < nb) load_block8<VEC>(src + bn * 64, l8, nlo, nhi);
         float mn, mx;
-        group_minmax(x, slot_shift, mn, mx);
+        group_minmax8(lo, hi, gbase, mn, mx);
         const float range = __fsub_rn(mx, mn);
         const float d = range / 15.0f;
         const float id = range > 0.0f ? 15.0f / range : 0.0f;
-        const uint32_t mine = q4(x.x, mn, id) | (q4(x.y, mn, id) << 8) |
-                              (q4(x.z, mn, id) << 16) | (q4(x.w, mn, id) << 24);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)mine, 8, 16);
+        const uint32_t b0 = q4(lo.x, mn, id) | (q4(hi.x, mn, id) << 4);
+        const uint32_t b1 = q4(lo.y, mn, id) | (q4(hi.y, mn, id) << 4);
+        const uint32_t b2 = q4(lo.z, mn, id) | (q4(hi.z, mn, id) << 4);
+        const uint32_t b3 = q4(lo.w, mn, id) | (q4(hi.w, mn, id) << 4);
         uint8_t *blk = dst + b * 40;
-        if (lane16 < 8) *reinterpret_cast<uint32_t *>(blk + lane16 * 4) = mine | (hi << 4);
-        if (lane16 == 0) {
+        *reinterpret_cast<uint32_t *>(blk + l8 * 4) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        if (l8 == 0) {
             *reinterpret_cast<float *>(blk + 32) = d;
             *reinterpret_cast<float *>(blk + 36) = mn;
         }
+        b = bn;
+        lo = nlo;
+        hi = nhi;
     }
 }
 
@@ -127,7 +146,9 @@ extern "C" int eakvd_ggml_quantize_row(const float *src, void *dst, int64_t k, v
 {
     const int64_t nb = k / 64;
     if (nb <= 0) return 0;
-    const dim3 grid(grid_for(nb * 16));
+    // 32 blocks per workgroup, one pass up to 2^16 workgroups
+    const int64_t wg = (nb + 31) / 32;
+    const dim3 grid((unsigned)(wg < 65536 ? wg : 65536));
     if ((uintptr_t)src % 16 == 0)
         hipLaunchKernelGGL(ggml_quantize_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
                            src, (uint8_t *)dst, nb);

@@ -27,32 +27,6 @@ namespace {
 constexpr int64_t kQuantBlocks = EAKV_QUANT_BLOCKS;
 constexpr int64_t kOnePass = 32768;
 
-// DPP moves within 8-lane groups: the mirror of each half row (lane i and
-// 7 - i), and the quad permutations xor 2 and xor 1.
-constexpr int kDppHalfMirror = 0x141, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v)
-{
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
-}
-
-// The first element of the group, in index order, that compares equal to
-// zero (the group has one): the low halves of lanes 0-7 hold elements 0-31,
-// the high halves 32-63.  gbase: the group's first lane in the wave.
-__device__ __forceinline__ float first_zero8(const float4 &lo, const float4 &hi, int gbase)
-{
-    const float zl = lo.x == 0.0f ? lo.x : (lo.y == 0.0f ? lo.y : (lo.z == 0.0f ? lo.z : lo.w));
-    const float zh = hi.x == 0.0f ? hi.x : (hi.y == 0.0f ? hi.y : (hi.z == 0.0f ? hi.z : hi.w));
-    const bool hl = (lo.x == 0.0f) | (lo.y == 0.0f) | (lo.z == 0.0f) | (lo.w == 0.0f);
-    const bool hh = (hi.x == 0.0f) | (hi.y == 0.0f) | (hi.z == 0.0f) | (hi.w == 0.0f);
-    const uint32_t bl = (uint32_t)(__ballot(hl) >> gbase) & 0xffu;
-    const uint32_t bh = (uint32_t)(__ballot(hh) >> gbase) & 0xffu;
-    const int sl = bl ? __ffs((int)bl) - 1 : 0;
-    const int sh = bh ? __ffs((int)bh) - 1 : 0;
-    const float vl = __shfl(zl, sl, 8), vh = __shfl(zh, sh, 8);
-    return bl ? vl : vh;
-}
-
 // One group: the reference's min/max, scale, bias and nibbles; lane j's
 // four packed bytes, and (lane 0) the scale and bias.
 struct QOut {
@@ -62,30 +36,8 @@ struct QOut {
 
 __device__ __forceinline__ QOut quantize_group8(const float4 &lo, const float4 &hi, int gbase)
 {
-    float mn = fminf(fminf(fminf(lo.x, lo.y), fminf(lo.z, lo.w)),
-                     fminf(fminf(hi.x, hi.y), fminf(hi.z, hi.w)));
-    float mx = fmaxf(fmaxf(fmaxf(lo.x, lo.y), fmaxf(lo.z, lo.w)),
-                     fmaxf(fmaxf(hi.x, hi.y), fmaxf(hi.z, hi.w)));
-    mn = fminf(mn, dpp_f<kDppHalfMirror>(mn));
-    mx = fmaxf(mx, dpp_f<kDppHalfMirror>(mx));
-    mn = fminf(mn, dpp_f<kDppXor2>(mn));
-    mx = fmaxf(mx, dpp_f<kDppXor2>(mx));
-    mn = fminf(mn, dpp_f<kDppXor1>(mn));
-    mx = fmaxf(mx, dpp_f<kDppXor1>(mx));
-    // a zero min or max: the first zero's sign, as a strict scan keeps it
-    if (mn == 0.0f || mx == 0.0f) {
-        const float z = first_zero8(lo, hi, gbase);
-        if (mn == 0.0f) mn = z;
-        if (mx == 0.0f) mx = z;
-    }
-    // a NaN element 0 makes min = max = that NaN
-    if (__ballot((threadIdx.x & 7) == 0 && lo.x != lo.x) != 0) {
-        const float x0 = __shfl(lo.x, 0, 8);
-        if (x0 != x0) {
-            mn = x0;
-            mx = x0;
-        }
-    }
+    float mn, mx;
+    group_minmax8(lo, hi, gbase, mn, mx);
     const float range = __fsub_rn(mx, mn);
     QOut o;
     o.scale = 1.0f;
