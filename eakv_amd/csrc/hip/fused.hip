@@ -14,10 +14,11 @@
 //
 // mfma_kernel (one or two quads of q heads per wave: up to 8 q heads per kv
 //   head; larger groups as virtual kv heads of at most 8 that share the kv
-//   head's tiles; also the unfused V-sum): waves walking 32-token tiles with
-//   two pipeline stages in flight.  Both products run on the int8
-//   matrix cores; on gfx950 matrix and vector instructions of a SIMD do not
-//   overlap, so the design minimises their sum:
+//   head's tiles; also the unfused V-sum): waves walking 32-token tiles,
+//   one or two groups of tile loads in flight behind the one consumed.
+//   Both products run on the int8 matrix cores; on gfx950 matrix and vector
+//   instructions of a SIMD do not overlap, so the design minimises their
+//   sum:
 //   K: per 16 tokens and 64-dim group one v_mfma_i32_16x16x64_i8, A = the q
 //     heads as 32-bit fixed point split into four signed bytes (rows 4h+p),
 //     B = the token's packed bytes masked to nibbles.  Exact integer dots,
@@ -61,21 +62,28 @@ constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
 #endif
 constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
 // Blocks of the kernel for HH quads of q heads per wave.  One quad: blocks
-// of kWaves waves, kBlocksPerCU resident per CU, tiles dealt statically.
-// Two quads: blocks of 8 waves (d = 128: one per CU, 2 waves per SIMD, as
-// the registers allow; d = 64: two) whose waves take their tiles from a
-// block counter in LDS.  A SIMD issues its older wave's instructions first,
-// so with a static deal the wave of the later block ran last, alone on its
-// SIMD; with the counter the waves of a block finish together.
+// of kWaves waves, kBlocksPerCU resident per CU.  Two quads: blocks of 8
+// waves (d = 128: one per CU, 2 waves per SIMD, as the registers allow;
+// d = 64: two).  Tiles are dealt statically in both, so every wave sums the
+// same tiles in the same order on every call and results are reproducible
+// bit for bit.
 template <int HH>
 constexpr int kWavesH = HH == 1 ? kWaves : 8;
 template <int D, int HH>
 constexpr int kBlocksPerCUH = HH == 1 ? kBlocksPerCU : (D == 64 ? 2 : 1);
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
+// Load groups per wave, one consumed and the rest in flight: 3 with one
+// quad per wave, 2 with two (twice the arithmetic per group covers the
+// latency; 64 q / 8 kv heads, d = 128, 131071 tokens: 39.2 against
+// 40.0-40.6 us per call with 3)
 #ifndef EAKV_FUSED_SLOTS
 #define EAKV_FUSED_SLOTS 3
 #endif
-constexpr int kSlots = EAKV_FUSED_SLOTS;  // load groups per wave: one consumed, the rest in flight
+#ifndef EAKV_FUSED_SLOTS2
+#define EAKV_FUSED_SLOTS2 2
+#endif
+template <int HH>
+constexpr int kSlotsH = HH == 1 ? EAKV_FUSED_SLOTS : EAKV_FUSED_SLOTS2;
 #ifndef EAKV_SHARE_Q
 #define EAKV_SHARE_Q 1
 #endif
@@ -499,6 +507,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     constexpr int NKL = VS ? NK * HH : kNK<D>;
     using StageT = std::conditional_t<VS, WStage<D, HH>, Stage<D>>;
     constexpr int NW = kWavesH<HH>;                     // waves per block
+    constexpr int kSlots = kSlotsH<HH>;                 // load groups per wave
     // Per wave: kSlots V and scale slots and the digit rows of its HH
     // quads; after the tiles the wave's V slots 0 (and 1) hold its outputs
     // o[4][D] of quad 0 (and 1) and its digit rows its m[8], l[8] for the
@@ -517,7 +526,6 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? NW : 1][Geo<D>::SSLOT];
     __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? NW : 1][Geo<D>::SSLOT];
     __shared__ __attribute__((aligned(16))) uint8_t z_lds[NW][HH * Geo<D>::ZROWS * 8];
-    __shared__ unsigned q_ctr;                          // claimed tiles (two quads)
 
     const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
@@ -532,10 +540,6 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
                     out[((int64_t)s * n_q + (int64_t)kvh * qpk) * D + i] = zo * (1.0f / zl);
             }
         return;
-    }
-    if constexpr (HH > 1) {
-        if (threadIdx.x == 0) q_ctr = 0;
-        __syncthreads();
     }
     // the wave index is wave-uniform: say so, so that every per-wave
     // quantity (token range, tile offsets) stays in scalar registers
@@ -658,31 +662,11 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     };
     using I0 = std::integral_constant<int, 0>;
 
-    // Tile schedule: tk[j] = T(i + j), the wave's tiles from the current
-    // one on.  T(j) = first + j * stride for j < kSlots; the later tiles
-    // are T(j) = first + j * stride too (one quad), or the block's claims
-    // (two quads): claim c is tile ch*NW + k%NW + (k/NW)*stride with
-    // k = kSlots*NW + c, so a wave's tiles still increase and the block's
-    // tiles are those of its static deal.
+    // Tile schedule: tk[j] = T(i + j) = first + (i + j) * stride, the
+    // wave's tiles from the current one on.
     int tk[kSlots + 1];
 #pragma unroll
     for (int j = 0; j < kSlots; j++) tk[j] = first + j * stride;
-    int ring[kSlots];
-    // lane 0 adds 1 to the block counter, the other lanes add 0 to words of
-    // this wave's digit rows (unchanged), so the add needs no branch
-    uint32_t *cptr = l == 0 ? &q_ctr : (uint32_t *)z_lds[w] + l;
-    const uint32_t cinc = l == 0 ? 1u : 0u;
-    auto fetch = [&](int &dst) {
-        if constexpr (HH > 1) {
-            dst = (int)__hip_atomic_fetch_add(cptr, cinc, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_WORKGROUP);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    auto claimed = [&](int c) {
-        const int k = kSlots * NW + __builtin_amdgcn_readfirstlane(c);
-        return ch * NW + k % NW + (k / NW) * stride;
-    };
     // token offset of a tile for loads: past-the-end tiles re-read the
     // unit's last tile (in bounds; their scores are masked)
     auto ldt = [&](int t) { return min(t, n_tiles - 1) * kTT; };
@@ -716,16 +700,9 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     if constexpr (VS) load_w<D, HH>(st[0], wr, wo, ldt(tk[0]), tl, L);
     else load_k<D>(st[0], P, ldt(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
-    fetch(ring[1]);
     load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
-    if constexpr (kSlots > 2) {
-        fetch(ring[2]);
-        load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
-    }
-    if constexpr (kSlots > 3) {
-        fetch(ring[3]);
-        load_group(std::integral_constant<int, 3>{}, tk[2], tk[3]);
-    }
+    if constexpr (kSlots > 2) load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
+    if constexpr (kSlots > 3) load_group(std::integral_constant<int, 3>{}, tk[2], tk[3]);
 
     // scores are kept in the log2 domain (times log2(e))
     const float rs2 = rs * EAKV_LOG2E;
@@ -1049,13 +1026,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             wait_vm<kDma<D> + NKL + kEarly>();
             VRead R;
             vread(vslot(rc), R);
-            if constexpr (HH == 1) {
-                tk[kSlots] = tk[kSlots - 1] + stride;
-            } else {
-                tk[kSlots] = claimed(ring[(r + 1) % kSlots]);
-                __builtin_amdgcn_sched_barrier(0);
-                fetch(ring[r]);
-            }
+            tk[kSlots] = tk[kSlots - 1] + stride;
             __builtin_amdgcn_sched_barrier(0);
             load_group(std::integral_constant<int, r + kSlots>{}, tk[kSlots - 1], tk[kSlots]);
             vsum(R);
@@ -1070,13 +1041,31 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             for (int j = 0; j < kSlots; j++) tk[j] = __builtin_amdgcn_readfirstlane(tk[j + 1]);
             return more;
         };
+        // The explicit waits above count the loads of every group in issue
+        // order, so each group's register loads must stay in the iteration
+        // that issues them.  The V-sum's weight loads, used only by the next
+        // iteration, were sunk by the compiler into that iteration's block
+        // (past the waits that count them, so a scale slot was read before
+        // its load had landed); using every weight stage on the exit path as
+        // well keeps them where they are.  (The K loads stay in place; the
+        // order of every loop block is checked on the compiled code by
+        // tests/test_isa_order.py.)
+        auto keep = [&]() {
+            if constexpr (VS)
+#pragma unroll
+                for (int j = 0; j < kSlots; j++)
+#pragma unroll
+                    for (int hq = 0; hq < HH; hq++)
+#pragma unroll
+                        for (int k = 0; k < NK; k++) asm volatile("" ::"v"(st[j].wv[hq][k]));
+        };
         for (;;) {
-            if (!iter(std::integral_constant<int, 0>{})) break;
-            if (!iter(std::integral_constant<int, 1>{})) break;
+            if (!iter(std::integral_constant<int, 0>{})) { keep(); break; }
+            if (!iter(std::integral_constant<int, 1>{})) { keep(); break; }
             if constexpr (kSlots > 2)
-                if (!iter(std::integral_constant<int, 2>{})) break;
+                if (!iter(std::integral_constant<int, 2>{})) { keep(); break; }
             if constexpr (kSlots > 3)
-                if (!iter(std::integral_constant<int, 3>{})) break;
+                if (!iter(std::integral_constant<int, 3>{})) { keep(); break; }
         }
     }
     // loads into LDS still in flight (the clamped groups past the end) must

@@ -244,6 +244,31 @@ def test_large_groups_fused_and_v_sum(E, rng, nh, n_q, n_kv, d, L, lmax):
     assert ok, (err, nbad)
 
 
+@pytest.mark.parametrize("nh,n_q,n_kv,d,L", [
+    (8, 64, 8, 128, 40000), (2, 16, 2, 64, 20000), (2, 12, 2, 128, 9000),
+    (4, 16, 4, 128, 30000)])
+def test_fused_repeat_bits_eight_heads(E, rng, nh, n_q, n_kv, d, L):
+    """Every wave of the matrix-core program sums a fixed set of tiles in a
+    fixed order, so a call repeated on the same inputs gives the same bits:
+    fused attention (against the oracle too) and the V-sum, at 5-8 q heads
+    per kv head (two quads per wave) and at 4 (one quad per wave), over
+    contexts long enough that every wave takes many tiles."""
+    say("repeat-bits", nh, n_q, n_kv, d, L)
+    g, o = loaded(E, rng, nh, d, L, L, nl=1)
+    q = (rng.standard_normal((n_q, d)) * 2).astype(np.float32)
+    a = g.attention_fused(q, 0, n_q, n_kv)
+    ok, err, nbad = tol_close(a, o.attention_fused(q, 0, n_q, n_kv), ATOL, RTOL)
+    assert ok, (err, nbad)
+    for _ in range(3):
+        assert np.array_equal(g.attention_fused(q, 0, n_q, n_kv).view(np.uint32),
+                              a.view(np.uint32))
+    w = rng.random((n_q, L)).astype(np.float32)
+    b = g.attention_output(w, 0, n_q, n_kv)
+    for _ in range(3):
+        assert np.array_equal(g.attention_output(w, 0, n_q, n_kv).view(np.uint32),
+                              b.view(np.uint32))
+
+
 @pytest.mark.parametrize("nh,n_q,n_kv,d,L,lmax", SHAPES)
 def test_fused_parity(E, rng, nh, n_q, n_kv, d, L, lmax):
     say("fused", nh, n_q, n_kv, d, L)
