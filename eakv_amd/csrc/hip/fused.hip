@@ -72,18 +72,15 @@ constexpr int kWavesH = HH == 1 ? kWaves : 8;
 template <int D, int HH>
 constexpr int kBlocksPerCUH = HH == 1 ? kBlocksPerCU : (D == 64 ? 2 : 1);
 constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 units)
-// Load groups per wave, one consumed and the rest in flight: 3 with one
-// quad per wave, 2 with two (twice the arithmetic per group covers the
-// latency; 64 q / 8 kv heads, d = 128, 131071 tokens: 39.2 against
-// 40.0-40.6 us per call with 3)
+// Load groups per wave: one consumed while the next is in flight.  With the
+// non-temporal plane loads, two measured faster than three: 64 q / 8 kv
+// heads, d = 128, 131071 tokens: 39.2 against 40.0-40.6 us per call;
+// 8 x 32Q/8KV at 32767 tokens: 65.7-66.0 against 66.1-68.6 (per-step
+// medians); 32Q/32KV at 8192 tokens: 14.0-14.3 against 15.0.
 #ifndef EAKV_FUSED_SLOTS
-#define EAKV_FUSED_SLOTS 3
+#define EAKV_FUSED_SLOTS 2
 #endif
-#ifndef EAKV_FUSED_SLOTS2
-#define EAKV_FUSED_SLOTS2 2
-#endif
-template <int HH>
-constexpr int kSlotsH = HH == 1 ? EAKV_FUSED_SLOTS : EAKV_FUSED_SLOTS2;
+constexpr int kSlots = EAKV_FUSED_SLOTS;
 #ifndef EAKV_SHARE_Q
 #define EAKV_SHARE_Q 1
 #endif
@@ -512,7 +509,6 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     constexpr int NKL = VS ? NK * HH : kNK<D>;
     using StageT = std::conditional_t<VS, WStage<D, HH>, Stage<D>>;
     constexpr int NW = kWavesH<HH>;                     // waves per block
-    constexpr int kSlots = kSlotsH<HH>;                 // load groups per wave
     // Per wave: kSlots V and scale slots and the digit rows of its HH
     // quads; after the tiles the wave's V slots 0 (and 1) hold its outputs
     // o[4][D] of quad 0 (and 1) and its digit rows its m[8], l[8] for the
