@@ -34,9 +34,9 @@ extern "C" {
 /* Bytes between two chunk counters: counters on separate 64-byte lines do
  * not serialize one another's atomics. */
 #define EAKVD_CTR_STRIDE 64
-/* Counters of a cache: one per kv head, and at least one per CU of the
- * device (a launch merges its chunks itself only when its grid is smaller
- * than the device, so its units fit). */
+/* Counters of a cache: one per kv head, and at least 256 (a fused launch
+ * merges its chunks itself when every (sequence, kv head) unit of the call
+ * has a counter in caches[0]; more units take a second launch). */
 #define EAKVD_CTR_MIN_SLOTS 256
 
 typedef struct {

@@ -33,8 +33,9 @@
 //     byte column per lane) by ds_read_b64_tr_b8; the digits of a are
 //     exchanged through LDS the same way.  sum p*bias per (head, group) is
 //     kept apart and added at the end.
-//   Waves are merged in LDS, chunks by merge_kernel (or, for a grid smaller
-//   than the device, by the last block of each unit in the same launch).
+//   Waves are merged in LDS; chunks by the last block of each unit in the
+//   same launch (up to 16 chunks per unit, counters given), else by
+//   merge_kernel or merge_parts_kernel in a second launch.
 // valu_kernel (caches whose (layer, kv) blocks are beyond the 32-bit buffer
 //   offsets of mfma_kernel, above 1 GiB; every group size has a split into
 //   virtual kv heads, at worst of one q head each): one lane per token for K
@@ -57,8 +58,12 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
+// One-quad blocks resident per CU (8 waves): fewer loads in flight per CU
+// read the planes faster than 4 blocks (16 waves), and a unit has half the
+// chunks to merge (8 x 32Q/8KV at 32767 tokens, merged in the launch: 63.1-64.5
+// against 64.3-67.5 us per call with 4 blocks and a merge launch)
 #ifndef EAKV_FUSED_BLOCKS_PER_CU
-#define EAKV_FUSED_BLOCKS_PER_CU 4
+#define EAKV_FUSED_BLOCKS_PER_CU 2
 #endif
 constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
 // Blocks of the kernel for HH quads of q heads per wave.  One quad: blocks
@@ -1133,7 +1138,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     }
     if (!ctr) return;
 
-    // ---- the chunk merge in this launch (small grids): every thread's
+    // ---- the chunk merge in this launch: every thread's
     // partial stores are complete (vmcnt 0) before the barrier, and so
     // before the block counts itself on its unit's counter; the block that
     // counts last reads the unit's partials after it, merges them into out
@@ -1621,16 +1626,18 @@ extern "C" int eakvd_scratch(void **p)
     return 0;
 }
 
-// The chunks merged in the main launch: where counters are given, the grid
-// is smaller than the device (the merge launch would be most of such a call;
-// on large grids the merging blocks' tail costs more than the launch) and a
-// unit has at most kInBatch chunks (one round trip of loads).
+// The chunks merged in the main launch: where counters are given, every
+// unit has a counter and at most kInBatch chunks (one round trip of loads).
+// The merging block's tail (its partial written through, a counter round
+// trip, the unit's partials read back) costs less than a dependent launch,
+// measured with 8 waves per CU; with 16 waves per CU (4 one-quad blocks, 16
+// chunks per unit) it cost more.
 bool merge_in_launch(const eakvd_geom *g, const void *ctr, int mc, int64_t units)
 {
 #ifdef EAKV_NO_MERGE_IN_LAUNCH
     return false;
 #endif
-    return ctr && units * mc < cu_count() && mc <= kInBatch && units <= g->ctr_slots;
+    return ctr && mc <= kInBatch && units <= g->ctr_slots;
 }
 
 extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,

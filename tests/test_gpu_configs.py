@@ -57,8 +57,8 @@ def mfma_chunks(L, units, qpk, d):
     """Chunks per (sequence, kv head) of the fused matrix-core program: the
     launch rule of fused.hip's mfma_blocks_per_unit (chunks of at least 512
     tokens, 256 when that leaves fewer blocks than CUs; resident blocks per
-    CU: 4 for up to 4 q heads per kv head, else 1 at d=128, 2 at d=64)."""
-    per_cu = 4 if qpk <= 4 else (1 if d == 128 else 2)
+    CU: 2 for up to 4 q heads per kv head, else 1 at d=128, 2 at d=64)."""
+    per_cu = 2 if qpk <= 4 else (1 if d == 128 else 2)
     cu = n_cu()
     slots = cu * per_cu
     nb = 1 if units >= slots else slots // units
