@@ -166,8 +166,12 @@ int eakvi_order_after(eakv_cache_t *const *caches, int n, void *st)
 {
     void *to[EAKVD_MAX_BATCH];
     int k = 0;
-    for (int i = 0; i < n && i < EAKVD_MAX_BATCH; i++)
-        if (caches[i]->stream != st) to[k++] = caches[i]->stream;
+    for (int i = 0; i < n && i < EAKVD_MAX_BATCH; i++) {
+        void *s = caches[i]->stream;
+        int seen = s == st;
+        for (int j = 0; j < k && !seen; j++) seen = to[j] == s;
+        if (!seen) to[k++] = s;
+    }
     return k ? order_wait(caches[0], st, to, k) : EAKV_OK;
 }
 
@@ -201,7 +205,8 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
 
     int e = eakvd_get_device(&c->device);
     if (e) goto hip_fail;
-    e = eakvd_stream_create(&c->stream);
+    /* the device's caches share one stream (eakvd_device_stream) */
+    e = eakvd_device_stream(c->device, &c->stream);
     if (e) goto hip_fail;
     /* created here so that ordering a batched call allocates nothing */
     e = eakvd_event_create(&c->order_event);
@@ -219,7 +224,6 @@ hip_fail:
     eakvi_hip_fail(e, "cache_create");
     if (c->dev) eakvd_free(c->dev);
     if (c->order_event) eakvd_event_destroy(c->order_event);
-    if (c->stream) eakvd_stream_destroy(c->stream);
     free(c);
     return NULL;
 }
@@ -235,7 +239,6 @@ void eakv_cache_free(eakv_cache_t *c)
     if (c->order_event) eakvd_event_destroy(c->order_event);
     if (c->work) eakvd_free(c->work);
     if (c->dev) eakvd_free(c->dev);
-    if (c->stream) eakvd_stream_destroy(c->stream);
     if (ok) eakvi_leave(prev);
     free(c);
 }

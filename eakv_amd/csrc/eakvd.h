@@ -61,8 +61,7 @@ int  eakvd_malloc(void **p, size_t n);
 int  eakvd_free(void *p);
 int  eakvd_host_malloc(void **p, size_t n);   /* pinned */
 int  eakvd_host_free(void *p);
-int  eakvd_stream_create(void **s);
-int  eakvd_stream_destroy(void *s);
+int  eakvd_device_stream(int dev, void **s);   /* the caches' stream of device dev */
 int  eakvd_stream_sync(void *s);
 int  eakvd_event_create(void **e);            /* no timing */
 int  eakvd_event_destroy(void *e);

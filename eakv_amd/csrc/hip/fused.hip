@@ -57,7 +57,13 @@ namespace {
 // ------------------------------------------------------------------ MFMA
 
 constexpr int kWaves = 4;
-constexpr int kTT = 32;                 // tokens per tile (one pipeline stage)
+// Tokens per tile (one pipeline stage), TT = 32 or 64 (tile_tokens).  One
+// quad of q heads per wave: 32; its waves read their planes faster in
+// 32-token pieces than in 64-token ones (8 x 32Q/8KV at 32767 tokens, two
+// tiles dealt together: 64.5 against 61.2 us per call).  Two quads, long
+// contexts: 64, so the V products of a tile are one v_mfma_i32_16x16x64_i8
+// per 16 dims, and each (head, group) is recombined and given a digit
+// exponent once per 64 tokens (20% fewer VALU instructions per token).
 // One-quad blocks resident per CU (8 waves): fewer loads in flight per CU
 // read the planes faster than 4 blocks (16 waves), and a unit has half the
 // chunks to merge (8 x 32Q/8KV at 32767 tokens, merged in the launch: 63.1-64.5
@@ -95,35 +101,42 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef __attribute__((address_space(3))) v2i *lds_v2i;
 
-// Tile geometry.  A plane stores a token's GPD groups of 32 packed bytes
-// contiguously (a row of RB bytes, UPT 16-byte units).  Loads to LDS move 16
-// bytes per lane, 1 KB per instruction.
-template <int D>
+// Tile geometry of TT-token tiles.  A plane stores a token's GPD groups of
+// 32 packed bytes contiguously (a row of RB bytes, UPT 16-byte units).
+// Loads to LDS move 16 bytes per lane, 1 KB per instruction.
+template <int D, int TT>
 struct Geo {
+    static_assert(TT == 32 || TT == 64, "32- or 64-token tiles");
     static constexpr int GPD = D / 64;
-    static constexpr int NK = kTT / 16;            // K sub-tiles of 16 tokens
+    static constexpr int NK = TT / 16;             // K sub-tiles of 16 tokens
+    static constexpr int NH = TT / 32;             // 32-token halves (V transposed reads)
     static constexpr int RB = 32 * GPD;            // bytes of a token's row
     static constexpr int UPT = RB / 16;            // 16-byte units per row
     static constexpr int TPC = 8 / GPD;            // tokens per 256 bytes
-    static constexpr int NVD = kTT * RB / 1024;    // V loads per tile
-    static constexpr int VSLOT = kTT * RB;         // LDS bytes of one V tile
-    static constexpr int SSLOT = 256;              // floats of one scale slot
-    static constexpr int ZROWS = GPD * 2 * kTT;    // 8-byte digit rows per tile
+    static constexpr int NVD = TT * RB / 1024;     // V loads per tile
+    static constexpr int VSLOT = TT * RB;          // LDS bytes of one V tile
+    static constexpr int LP = TT * GPD / 4;        // lanes per scale plane piece (16 B each)
+    static constexpr int SSLOT = 4 * TT * GPD > 256 ? 4 * TT * GPD : 256;  // floats of a scale slot
+    static constexpr int NSL = SSLOT * 4 / 1024;   // scale loads per tile
+    static constexpr int ZROWS = GPD * 2 * TT;     // 8-byte digit rows per tile
 };
 
 // V tile layout in LDS: token rows in order, the 16-byte units of row t
 // permuted by xor with vswz(t) (bits of the token's 4-token / 8-token
 // block).  With the transposed reads below, that puts the 64 lanes' 8-byte
 // rows of one read on 32 distinct bank pairs (2 lanes each, the minimum),
-// and keeps each 16-byte unit whole for the 16-byte loads.
+// and keeps each 16-byte unit whole for the 16-byte loads.  vswz(t + 32) =
+// vswz(t), so the second half of a 64-token tile has the same pattern.
 template <int D>
 __device__ __host__ constexpr int vswz(int t)
 {
-    return (t / Geo<D>::TPC) & (Geo<D>::UPT - 1);
+    return (t / Geo<D, 32>::TPC) & (Geo<D, 32>::UPT - 1);
 }
 
-// The tile's token of byte j (0..7) of a V operand in lane group kq
-// (lanes 16kq..16kq+15).  Digits (A) and nibbles (B) use the same order.
+// The token (within a 32-token half) of byte j (0..7) of a V operand in
+// lane group kq (lanes 16kq..16kq+15).  Digits (A) and nibbles (B) use the
+// same order; in a 64-token tile, bytes 8..15 of a lane's operand are the
+// same tokens of the second half.
 __device__ __forceinline__ int vtok(int kq, int j)
 {
     return 16 * (j & 1) + 4 * kq + (j >> 1);
@@ -132,24 +145,24 @@ __device__ __forceinline__ int vtok(int kq, int j)
 // One lane's K bytes of a pipeline stage (MFMA B layout: token 16k + tl of
 // sub-tile k, bytes 8qq..8qq+7 of each group).  The V bytes and the K and V
 // scales and biases of a stage go to LDS.
-template <int D>
+template <int D, int TT>
 struct Stage {
-    uint2 kw[Geo<D>::NK][Geo<D>::GPD];
+    uint2 kw[Geo<D, TT>::NK][Geo<D, TT>::GPD];
 };
 
 // V-sum mode: one lane's weights of a pipeline stage (score layout: head
 // 4hq + l/16 of quad hq, token 16k + l%16 of sub-tile k).
-template <int D, int HH>
+template <int D, int HH, int TT>
 struct WStage {
-    float wv[HH][Geo<D>::NK];
+    float wv[HH][Geo<D, TT>::NK];
 };
 
 // The scales and biases of one tile for this lane's tokens (score layout:
 // token 16k + tl), read from the LDS slot.
-template <int D>
+template <int D, int TT>
 struct Scales {
-    float ks[Geo<D>::NK][Geo<D>::GPD], kb[Geo<D>::NK][Geo<D>::GPD];
-    float vs[Geo<D>::NK][Geo<D>::GPD], vb[Geo<D>::NK][Geo<D>::GPD];
+    float ks[Geo<D, TT>::NK][Geo<D, TT>::GPD], kb[Geo<D, TT>::NK][Geo<D, TT>::GPD];
+    float vs[Geo<D, TT>::NK][Geo<D, TT>::GPD], vb[Geo<D, TT>::NK][Geo<D, TT>::GPD];
 };
 
 // Buffer resources of the planes (scalar registers) and this lane's byte
@@ -158,7 +171,7 @@ struct Scales {
 // Reads past a plane's end return 0.
 struct LaneOffs {
     __amdgpu_buffer_rsrc_t kw, vw, layer;
-    uint32_t kwo, vwo, sco;
+    uint32_t kwo, vwo, sco[2];
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void *p, int64_t bytes)
@@ -180,17 +193,17 @@ __device__ __forceinline__ uint2 ldb64(__amdgpu_buffer_rsrc_t r, uint32_t vo, ui
 }
 
 // K bytes of the tile at token offset dt of the wave.  A tile can run up to
-// kTT - 1 tokens past the wave's last token; those reads stay inside the
+// TT - 1 tokens past the wave's last token; those reads stay inside the
 // plane (or return 0 beyond it), their scores are masked to -inf and their
 // weight is exactly 0.  dt is the same in every lane; readfirstlane makes
 // that visible, so the tile offset goes to the scalar soffset operand.
-template <int D>
-__device__ __forceinline__ void load_k(Stage<D> &T, const LaneOffs &P, int dt)
+template <int D, int TT>
+__device__ __forceinline__ void load_k(Stage<D, TT> &T, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
     const uint32_t ws = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 32;
 #pragma unroll
-    for (int k = 0; k < Geo<D>::NK; k++)
+    for (int k = 0; k < Geo<D, TT>::NK; k++)
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
             T.kw[k][gg] = ldb64(P.kw, P.kwo, ws + (16 * k * GPD + gg) * 32);
@@ -200,14 +213,14 @@ __device__ __forceinline__ void load_k(Stage<D> &T, const LaneOffs &P, int dt)
 // tl] from the kv head's rows (wo[hq]: byte offset of the lane's row).
 // Tokens past the sequence read the row's last weight (in bounds); the
 // caller masks them.
-template <int D, int HH>
-__device__ __forceinline__ void load_w(WStage<D, HH> &T, __amdgpu_buffer_rsrc_t r,
+template <int D, int HH, int TT>
+__device__ __forceinline__ void load_w(WStage<D, HH, TT> &T, __amdgpu_buffer_rsrc_t r,
                                        const uint32_t *wo, int dt, int tl, int L)
 {
 #pragma unroll
     for (int hq = 0; hq < HH; hq++)
 #pragma unroll
-        for (int k = 0; k < Geo<D>::NK; k++) {
+        for (int k = 0; k < Geo<D, TT>::NK; k++) {
             const int t = min(dt + 16 * k + tl, L - 1);
             T.wv[hq][k] = __uint_as_float(
                 __builtin_amdgcn_raw_buffer_load_b32(r, (int)(wo[hq] + 4u * (uint32_t)t), 0, 0));
@@ -217,39 +230,42 @@ __device__ __forceinline__ void load_w(WStage<D, HH> &T, __amdgpu_buffer_rsrc_t 
 // The V bytes of the tile at dt into a V slot, 1 KB per instruction (buffer
 // load to LDS: lane m's 16 bytes land at the instruction's LDS start + 16m;
 // the lane fetches the unit that belongs there, see LaneOffs.vwo).
-template <int D>
+template <int D, int TT>
 __device__ __forceinline__ void load_v(uint8_t *vslot, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
     const uint32_t ws = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 32;
 #pragma unroll
-    for (int i = 0; i < Geo<D>::NVD; i++)
+    for (int i = 0; i < Geo<D, TT>::NVD; i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(P.vw, (lds_ptr)(vslot + 1024 * i), 16,
                                                  (int)P.vwo, (int)(ws + 1024 * i), 0, kPlaneAux);
 }
 
-// The K and V scales and biases of the tile at dt into a scale slot, one
-// instruction.  Slot layout: plane p in {ks, kb, vs, vb} at p * kTT * GPD
-// floats, then token-major, group-minor, as in the planes (lane m fetches
-// 16 bytes of plane m / (8 GPD); at d=64 lanes 32-63 repeat lanes 0-31 into
-// the unused second half of the slot).
-template <int D>
+// The K and V scales and biases of the tile at dt into a scale slot, NSL
+// instructions (one, or two for 64 tokens at d=128).  Slot layout: plane p
+// in {ks, kb, vs, vb} at p * TT * GPD floats, then token-major,
+// group-minor, as in the planes; each plane piece is LP lanes of 16 bytes
+// (instruction i, lane m: plane (64i + m) / LP; at d=64 with 32-token tiles
+// lanes 32-63 repeat lanes 0-31 into the unused second half of the slot).
+template <int D, int TT>
 __device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int dt)
 {
     constexpr int GPD = D / 64;
     const uint32_t ss = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 4;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(P.layer, (lds_ptr)slot, 16, (int)P.sco,
-                                             (int)ss, 0, kPlaneAux);
+#pragma unroll
+    for (int i = 0; i < Geo<D, TT>::NSL; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(P.layer, (lds_ptr)(slot + 256 * i), 16,
+                                                 (int)P.sco[i], (int)ss, 0, kPlaneAux);
 }
 
 // Loads per group, in issue order: V chunks, scales, then the K bytes (or
 // the V-sum's weights; fixed by sched barriers).  The compiler does not order LDS reads after buffer loads to
 // LDS, so reads of a slot are preceded by an explicit wait for every load
 // older than the ones that may still be outstanding.
-template <int D>
-constexpr int kDma = 1;                                  // scale loads
-template <int D>
-constexpr int kNK = Geo<D>::NK * (D / 64);               // K loads
+template <int D, int TT>
+constexpr int kDma = Geo<D, TT>::NSL;                    // scale loads
+template <int D, int TT>
+constexpr int kNK = Geo<D, TT>::NK * (D / 64);           // K loads
 
 // s_waitcnt vmcnt(n), no wait on the other counters (gfx9 encoding:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -260,12 +276,12 @@ __device__ __forceinline__ void wait_vm()
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int D>
-__device__ __forceinline__ void read_scales(const float *slot, int tl, Scales<D> &C)
+template <int D, int TT>
+__device__ __forceinline__ void read_scales(const float *slot, int tl, Scales<D, TT> &C)
 {
-    constexpr int GPD = D / 64, PS = kTT * GPD;
+    constexpr int GPD = D / 64, PS = TT * GPD;
 #pragma unroll
-    for (int k = 0; k < Geo<D>::NK; k++) {
+    for (int k = 0; k < Geo<D, TT>::NK; k++) {
         const int e = (16 * k + tl) * GPD;
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++) {
@@ -351,12 +367,12 @@ __device__ __forceinline__ long as_long(v2i v)
 // H = 256*d0 + d1 and Lo = 256*d2 + d3 (|H|, |Lo| < 2^25), and
 // u = H*wh + Lo*wl with wh = 2^16*wl, wl = 2^-e*log2(e)/sqrt(d).  Scores are
 // in the log2 domain: sc = log2(e) * (q.k)/sqrt(d); masked tokens get -inf.
-template <int D>
-__device__ __forceinline__ void k_mfma(const Stage<D> &T, const v4i *A,
+template <int D, int TT>
+__device__ __forceinline__ void k_mfma(const Stage<D, TT> &T, const v4i *A,
                                        v4i (*dk)[D / 64])
 {
 #pragma unroll
-    for (int k = 0; k < Geo<D>::NK; k++)
+    for (int k = 0; k < Geo<D, TT>::NK; k++)
 #pragma unroll
         for (int gg = 0; gg < D / 64; gg++) {
             const uint2 raw = T.kw[k][gg];
@@ -367,8 +383,8 @@ __device__ __forceinline__ void k_mfma(const Stage<D> &T, const v4i *A,
         }
 }
 
-template <int D>
-__device__ __forceinline__ float k_recomb(const Scales<D> &T, const v4i *d, int k,
+template <int D, int TT>
+__device__ __forceinline__ float k_recomb(const Scales<D, TT> &T, const v4i *d, int k,
                                           int dt, int L, float wh, float wl,
                                           const float *bq, int tl)
 {
@@ -384,11 +400,15 @@ __device__ __forceinline__ float k_recomb(const Scales<D> &T, const v4i *d, int 
 }
 
 // The V accumulation of one (group, 16-byte column block) of a tile: one
-// transposed read gives each lane 8 tokens' bytes at byte column 16*half + n
-// of group g; the low nibbles are dims 64g + 16half + n, the high nibbles
-// dims 64g + 32 + 16half + n.  Each MFMA sums the 32 tokens of the tile; the
-// four digit rows of a head come back in one lane (C[i], weight 256^i) and
-// are recombined as (256*C3 + C2) * 2^(16-E) + (256*C1 + C0) * 2^-E.
+// transposed read per 32-token half gives each lane 8 tokens' bytes at byte
+// column 16*half + n of group g; the low nibbles are dims 64g + 16half + n,
+// the high nibbles dims 64g + 32 + 16half + n.  Each MFMA sums the tokens of
+// the tile (v_mfma_i32_16x16x32_i8 for 32, _16x16x64_i8 for 64); the four
+// digit rows of a head come back in one lane (C[i], weight 256^i) and are
+// recombined as (256*C3 + C2) * 2^(16-E) + (256*C1 + C0) * 2^-E.  The top
+// digit of a weight below 2^30 lies in [-64, 64], so |256*C3 + C2| < 2^24
+// and its conversion is exact; 256*C1 + C0 may round (64 tokens), 2^16
+// times below it.
 __device__ __forceinline__ float v_recomb(v4i c, float wh, float wl, float acc)
 {
     const int hi = c[3] * 256 + c[2];
@@ -483,7 +503,7 @@ __device__ __forceinline__ float vs_chunk_sum(const float *p, int n_chunks, int 
 }
 
 // Tile assignment: nb = gridDim.x blocks share one (sequence, kv head), a
-// "unit" of n_tiles kTT-token tiles, dealt round robin: tile j to block
+// "unit" of n_tiles TT-token tiles, dealt round robin: tile j to block
 // (j / kWaves) % nb and wave j % kWaves.  At any time the waves of a unit
 // read one contiguous window of every plane, and a wave's tiles are
 // nb * kWaves tiles apart.  Softmax partials do not depend on which tokens a
@@ -502,17 +522,18 @@ __device__ __forceinline__ float vs_chunk_sum(const float *p, int n_chunks, int 
 // digit rows (signed fixed point, the exponent from the largest |a|); m
 // stays 0, vsum_merge_kernel adds the chunks unnormalised, and a non-finite
 // weight makes its head's output NaN (lsum carries the flag).
-template <int D, int HH, bool VS>
+template <int D, int HH, bool VS, int TT>
 __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, HH> / 4)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
     int n_q, int qpk, float rs, float *__restrict__ part, int split,
     float *__restrict__ out, uint8_t *__restrict__ ctr)
 {
     constexpr int GPD = D / 64;
-    constexpr int NK = Geo<D>::NK;
+    constexpr int NK = Geo<D, TT>::NK;
+    constexpr int NH = Geo<D, TT>::NH;                  // 32-token halves
     // VGPR loads per group after the V and scale loads: K bytes, or weights
-    constexpr int NKL = VS ? NK * HH : kNK<D>;
-    using StageT = std::conditional_t<VS, WStage<D, HH>, Stage<D>>;
+    constexpr int NKL = VS ? NK * HH : kNK<D, TT>;
+    using StageT = std::conditional_t<VS, WStage<D, HH, TT>, Stage<D, TT>>;
     constexpr int NW = kWavesH<HH>;                     // waves per block
     // Per wave: kSlots V and scale slots and the digit rows of its HH
     // quads; after the tiles the wave's V slots 0 (and 1) hold its outputs
@@ -520,22 +541,22 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // block merge.  Every slot is its own variable: the
     // compiler then knows that a load into one slot does not write another
     // and does not make reads of a slot wait for younger loads to LDS.
-    static_assert(Geo<D>::VSLOT >= 4 * D * 4, "outputs fit a V slot");
+    static_assert(Geo<D, TT>::VSLOT >= 4 * D * 4, "outputs fit a V slot");
     static_assert(HH == 1 || HH == 2, "one or two quads");
     static_assert(kSlots <= 4, "slot variables");
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds0[NW][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds1[NW][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds2[kSlots > 2 ? NW : 1][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds3[kSlots > 3 ? NW : 1][Geo<D>::VSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds0[NW][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds1[NW][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? NW : 1][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? NW : 1][Geo<D>::SSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t z_lds[NW][HH * Geo<D>::ZROWS * 8];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds0[NW][Geo<D, TT>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds1[NW][Geo<D, TT>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds2[kSlots > 2 ? NW : 1][Geo<D, TT>::VSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t v_lds3[kSlots > 3 ? NW : 1][Geo<D, TT>::VSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds0[NW][Geo<D, TT>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds1[NW][Geo<D, TT>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? NW : 1][Geo<D, TT>::SSLOT];
+    __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? NW : 1][Geo<D, TT>::SSLOT];
+    __shared__ __attribute__((aligned(16))) uint8_t z_lds[NW][HH * Geo<D, TT>::ZROWS * 8];
 
     const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
     const int L = bt.seq_len[s];
-    const int n_tiles = (L + kTT - 1) / kTT;
+    const int n_tiles = (L + TT - 1) / TT;
     if (ch * NW >= n_tiles) {         // no tile for this block: no partial
         // merged here, an empty sequence's outputs are 0 * (1/0) = NaN, as
         // the reference's (and merge_kernel's)
@@ -609,18 +630,22 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         // K and V blocks of the layer are adjacent: one resource for the
         // scale and bias planes of both
         P.layer = plane_rsrc(K.w, 2 * g.block_bytes);
-        // scale load: lane l fetches bytes 16e.. of plane pl's tile
+        // scale load i: lane l fetches bytes 16e.. of plane pl's tile
         // (V-sum: only the V planes; lanes of the K planes fetch them again)
-        const int pl = (GPD == 2 ? l >> 4 : (l & 31) >> 3) | (VS ? 2 : 0);
-        const int e = GPD == 2 ? l & 15 : l & 7;
-        const int64_t poff = (pl & 2 ? g.block_bytes : 0) + (pl & 1 ? g.b_off : g.s_off);
-        P.sco = (uint32_t)(poff + hbase * 4 + 16 * e);
+        constexpr int LP = Geo<D, TT>::LP;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int pl = (((64 * i + l) / LP) & 3) | (VS ? 2 : 0);
+            const int e = l % LP;
+            const int64_t poff = (pl & 2 ? g.block_bytes : 0) + (pl & 1 ? g.b_off : g.s_off);
+            P.sco[i] = (uint32_t)(poff + hbase * 4 + 16 * e);
+        }
         P.kwo = (uint32_t)((hbase + (int64_t)tl * GPD) * 32 + qq * 8);
         // V load: lane l's 16 bytes land at unit l of the first 1 KB of the
         // slot: token t = l / UPT, unit (l % UPT) of the permuted row
-        const int vt = l / Geo<D>::UPT;
-        const int vu = (l % Geo<D>::UPT) ^ vswz<D>(vt);
-        P.vwo = (uint32_t)(hbase * 32 + vt * Geo<D>::RB + 16 * vu);
+        const int vt = l / Geo<D, TT>::UPT;
+        const int vu = (l % Geo<D, TT>::UPT) ^ vswz<D>(vt);
+        P.vwo = (uint32_t)(hbase * 32 + vt * Geo<D, TT>::RB + 16 * vu);
         if constexpr (VS) {
             // lane (ho, tl): row kvh*qpk + 4hq + ho (head 0 past the group), token tl
 #pragma unroll
@@ -645,10 +670,10 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
             for (int half = 0; half < 2; half++)
-                vrd[gg][half] = (uint32_t)(t * Geo<D>::RB +
+                vrd[gg][half] = (uint32_t)(t * Geo<D, TT>::RB +
                                            16 * ((2 * gg + half) ^ vswz<D>(t)) + 8 * (rr & 1));
-        zrd = (uint32_t)(((rr & 1) * kTT + t) * 8);
-        zwr = (uint32_t)(((ho >> 1) * kTT + tl) * 8 + 4 * (ho & 1));
+        zrd = (uint32_t)(((rr & 1) * TT + t) * 8);
+        zwr = (uint32_t)(((ho >> 1) * TT + tl) * 8 + 4 * (ho & 1));
     }
     uint8_t *zb = z_lds[w];
     // slot k of this wave (k a constant)
@@ -675,19 +700,19 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     for (int j = 0; j < kSlots; j++) tk[j] = first + j * stride;
     // token offset of a tile for loads: past-the-end tiles re-read the
     // unit's last tile (in bounds; their scores are masked)
-    auto ldt = [&](int t) { return min(t, n_tiles - 1) * kTT; };
+    auto ldt = [&](int t) { return min(t, n_tiles - 1) * TT; };
 
     StageT st[kSlots];
     // group j: V of tile T(j-1) into V slot (j-1) % kSlots, then the scales
     // and K bytes of tile T(j) into scale slot and stage j % kSlots
     auto load_group = [&](auto jc, int tv, int tkk) {
         constexpr int j = decltype(jc)::value;
-        load_v<D>(vslot(std::integral_constant<int, (j + kSlots - 1) % kSlots>{}), P, ldt(tv));
+        load_v<D, TT>(vslot(std::integral_constant<int, (j + kSlots - 1) % kSlots>{}), P, ldt(tv));
         __builtin_amdgcn_sched_barrier(0);
-        load_scales<D>(sslot(std::integral_constant<int, j % kSlots>{}), P, ldt(tkk));
+        load_scales<D, TT>(sslot(std::integral_constant<int, j % kSlots>{}), P, ldt(tkk));
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (VS) load_w<D, HH>(st[j % kSlots], wr, wo, ldt(tkk), tl, L);
-        else load_k<D>(st[j % kSlots], P, ldt(tkk));
+        if constexpr (VS) load_w<D, HH, TT>(st[j % kSlots], wr, wo, ldt(tkk), tl, L);
+        else load_k<D, TT>(st[j % kSlots], P, ldt(tkk));
         __builtin_amdgcn_sched_barrier(0);
     };
     // Unconditional (a wave without tiles reads the unit's last tile), so
@@ -701,10 +726,10 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         P.vw, (lds_ptr)vslot(std::integral_constant<int, kSlots - 1>{}), 4, (int)P.vwo,
         (int)((uint32_t)__builtin_amdgcn_readfirstlane(ldt(tk[0])) * GPD * 32), 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    load_scales<D>(sslot(I0{}), P, ldt(tk[0]));
+    load_scales<D, TT>(sslot(I0{}), P, ldt(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (VS) load_w<D, HH>(st[0], wr, wo, ldt(tk[0]), tl, L);
-    else load_k<D>(st[0], P, ldt(tk[0]));
+    if constexpr (VS) load_w<D, HH, TT>(st[0], wr, wo, ldt(tk[0]), tl, L);
+    else load_k<D, TT>(st[0], P, ldt(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
     load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
     if constexpr (kSlots > 2) load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
@@ -820,11 +845,11 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // with E = 30 - (exponent of the tile's largest a of the head and
     // group), so 0 <= z < 2^30.  The balanced digits of z go to the digit
     // rows; wh/wl are 2^(16-E) and 2^-E.
-    auto weights = [&](auto hqc, const Scales<D> &C, const float *sc, float m, float &psum,
+    auto weights = [&](auto hqc, const Scales<D, TT> &C, const float *sc, float m, float &psum,
                        float *bi) {
         constexpr int hq = decltype(hqc)::value;
         WaveState<D> &Sq = S[hq];
-        uint8_t *zq = zb + hq * Geo<D>::ZROWS * 8;
+        uint8_t *zq = zb + hq * Geo<D, TT>::ZROWS * 8;
         float p[NK];
         psum = 0.0f;
 #pragma unroll
@@ -850,7 +875,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             for (int k = 0; k < NK; k++) {
                 const int z = (int)__builtin_amdgcn_ldexpf(a[k], E);
                 const uint32_t u = ((uint32_t)z + 0x80808080u) ^ 0x80808080u;
-                *(uint32_t *)(zq + zwr + gg * 2 * kTT * 8 + k * 16 * 8) = u;
+                *(uint32_t *)(zq + zwr + gg * 2 * TT * 8 + k * 16 * 8) = u;
             }
             Sq.wl[gg] = __builtin_amdgcn_ldexpf(1.0f, -E);
             Sq.wh[gg] = __builtin_amdgcn_ldexpf(1.0f, 16 - E);
@@ -864,7 +889,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // weights; otherwise (rare: the first tile, a new larger score) the
     // moved maxima are set and the accumulators scaled by 2^(old - new)
     // first.
-    auto softmax = [&](const Scales<D> &C, float (*sc)[NK]) {
+    auto softmax = [&](const Scales<D, TT> &C, float (*sc)[NK]) {
         bool need[HH];
         float mt[HH];
         bool any = false;
@@ -909,15 +934,15 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
 
     // K(tile at dt) from its stage and scale slot: the scores of the tile
     // for every quad, then each quad's softmax.
-    auto kscores_softmax = [&](const Stage<D> &T, const Scales<D> &C, int dt) {
+    auto kscores_softmax = [&](const Stage<D, TT> &T, const Scales<D, TT> &C, int dt) {
         float sc[HH][NK];
 #pragma unroll
         for (int hq = 0; hq < HH; hq++) {
             v4i dk[NK][GPD];
-            k_mfma<D>(T, A[hq], dk);
+            k_mfma<D, TT>(T, A[hq], dk);
 #pragma unroll
             for (int k = 0; k < NK; k++)
-                sc[hq][k] = k_recomb<D>(C, dk[k], k, dt, L, kwh[hq], kwl[hq], bq[hq], tl);
+                sc[hq][k] = k_recomb<D, TT>(C, dk[k], k, dt, L, kwh[hq], kwl[hq], bq[hq], tl);
         }
         softmax(C, sc);
     };
@@ -925,7 +950,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // V-sum: the weights of the tile at dt (past the sequence and for heads
     // past the group: 0) to the digit rows, sum w*bias per (head, group) to
     // bacc; a non-finite weight sets the head's lsum to NaN.
-    auto vs_weights = [&](const auto &T, const Scales<D> &C, int dt) {
+    auto vs_weights = [&](const auto &T, const Scales<D, TT> &C, int dt) {
         float pw[HH][NK];
         bool bad[HH];
 #pragma unroll
@@ -953,33 +978,54 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     };
 
     // V(tile in vslot) with the digits in the digit rows: the transposed
-    // reads (vread), then the 4*GPD MFMA pairs, then their recombination, so
-    // the MFMA latency is covered by the MFMAs behind it (vsum).
+    // reads (vread; NH per operand, one per 32-token half, bytes 8h..8h+7 of
+    // a lane's operand from half h), then the 4*GPD MFMA pairs, then their
+    // recombination, so the MFMA latency is covered by the MFMAs behind it
+    // (vsum).
     struct VRead {
-        v2i az[HH][GPD], x[GPD][2];
+        v2i az[HH][GPD][NH], x[GPD][2][NH];
     };
     auto vread = [&](const uint8_t *vslot, VRead &R) {
 #pragma unroll
         for (int hq = 0; hq < HH; hq++)
 #pragma unroll
             for (int gg = 0; gg < GPD; gg++)
-                R.az[hq][gg] = tr8(zb + hq * Geo<D>::ZROWS * 8 + zrd + gg * 2 * kTT * 8);
+#pragma unroll
+                for (int h = 0; h < NH; h++)
+                    R.az[hq][gg][h] = tr8(zb + hq * Geo<D, TT>::ZROWS * 8 + zrd +
+                                          gg * 2 * TT * 8 + h * 32 * 8);
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
             for (int half = 0; half < 2; half++)
-                R.x[gg][half] = tr8(vslot + vrd[gg][half]);
+#pragma unroll
+                for (int h = 0; h < NH; h++)
+                    R.x[gg][half][h] = tr8(vslot + vrd[gg][half] + h * 32 * Geo<D, TT>::RB);
+    };
+    // the MFMA of one operand pair: 32 tokens (8 bytes per lane) or 64 (16)
+    auto vmfma = [](const v2i *a, const v2i *b) -> v4i {
+        if constexpr (NH == 1)
+            return __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a[0]), as_long(b[0]),
+                                                         v4i{0, 0, 0, 0}, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{a[0][0], a[0][1], a[1][0], a[1][1]},
+                                                         v4i{b[0][0], b[0][1], b[1][0], b[1][1]},
+                                                         v4i{0, 0, 0, 0}, 0, 0, 0);
     };
     auto vsum = [&](const VRead &R) {
         const auto &x = R.x;
-        v2i lo[GPD][2], hi[GPD][2];
+        v2i lo[GPD][2][NH], hi[GPD][2][NH];
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
-            for (int half = 0; half < 2; half++) {
-                lo[gg][half] = v2i{(int)nib_lo(x[gg][half][0]), (int)nib_lo(x[gg][half][1])};
-                hi[gg][half] = v2i{(int)nib_hi(x[gg][half][0]), (int)nib_hi(x[gg][half][1])};
-            }
+            for (int half = 0; half < 2; half++)
+#pragma unroll
+                for (int h = 0; h < NH; h++) {
+                    lo[gg][half][h] = v2i{(int)nib_lo(x[gg][half][h][0]),
+                                          (int)nib_lo(x[gg][half][h][1])};
+                    hi[gg][half][h] = v2i{(int)nib_hi(x[gg][half][h][0]),
+                                          (int)nib_hi(x[gg][half][h][1])};
+                }
 #pragma unroll
         for (int hq = 0; hq < HH; hq++) {
             const auto &az = R.az[hq];
@@ -988,10 +1034,8 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             for (int gg = 0; gg < GPD; gg++)
 #pragma unroll
                 for (int half = 0; half < 2; half++) {
-                    c[gg][half][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                        as_long(az[gg]), as_long(lo[gg][half]), v4i{0, 0, 0, 0}, 0, 0, 0);
-                    c[gg][half][1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                        as_long(az[gg]), as_long(hi[gg][half]), v4i{0, 0, 0, 0}, 0, 0, 0);
+                    c[gg][half][0] = vmfma(az[gg], lo[gg][half]);
+                    c[gg][half][1] = vmfma(az[gg], hi[gg][half]);
                 }
             WaveState<D> &Sq = S[hq];
 #pragma unroll
@@ -1012,24 +1056,24 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // V(T(i)) and K(T(i+1)) with its softmax (digits of T(i+1)).  kSlots-1
     // groups stay in flight behind the one consumed (rotating registers and
     // LDS slots).
-    constexpr int kGrp = Geo<D>::NVD + kDma<D> + NKL;   // loads per group
+    constexpr int kGrp = Geo<D, TT>::NVD + kDma<D, TT> + NKL;   // loads per group
     constexpr int kLater = (kSlots - 1) * kGrp;         // loads of the groups after the oldest
     constexpr int kEarly = (kSlots - 2) * kGrp;
     if (tk[0] < n_tiles) {
         {
-            Scales<D> C;
+            Scales<D, TT> C;
             // group 0 (scales, K of T(0)) is complete once at most its K
             // loads and all later groups are outstanding
             wait_vm<NKL + kLater>();
-            read_scales<D>(sslot(I0{}), tl, C);
-            if constexpr (VS) vs_weights(st[0], C, tk[0] * kTT);
-            else kscores_softmax(st[0], C, tk[0] * kTT);
+            read_scales<D, TT>(sslot(I0{}), tl, C);
+            if constexpr (VS) vs_weights(st[0], C, tk[0] * TT);
+            else kscores_softmax(st[0], C, tk[0] * TT);
         }
         // iteration i = r (mod kSlots)
         auto iter = [&](auto rc) {
             constexpr int r = decltype(rc)::value;
             // V(T(i)): its loads were the first of group i+1
-            wait_vm<kDma<D> + NKL + kEarly>();
+            wait_vm<kDma<D, TT> + NKL + kEarly>();
             VRead R;
             vread(vslot(rc), R);
             tk[kSlots] = tk[kSlots - 1] + stride;
@@ -1037,11 +1081,11 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             load_group(std::integral_constant<int, r + kSlots>{}, tk[kSlots - 1], tk[kSlots]);
             vsum(R);
             // K(T(i+1)): scales, then bytes (the compiler waits for those)
-            Scales<D> C;
+            Scales<D, TT> C;
             wait_vm<NKL + kLater>();
-            read_scales<D>(sslot(std::integral_constant<int, (r + 1) % kSlots>{}), tl, C);
-            if constexpr (VS) vs_weights(st[(r + 1) % kSlots], C, tk[1] * kTT);
-            else kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * kTT);
+            read_scales<D, TT>(sslot(std::integral_constant<int, (r + 1) % kSlots>{}), tl, C);
+            if constexpr (VS) vs_weights(st[(r + 1) % kSlots], C, tk[1] * TT);
+            else kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * TT);
             const bool more = tk[1] < n_tiles;
 #pragma unroll
             for (int j = 0; j < kSlots; j++) tk[j] = __builtin_amdgcn_readfirstlane(tk[j + 1]);
@@ -1175,12 +1219,13 @@ constexpr int kMergeBatch = 16;
 
 template <int D>
 __global__ __launch_bounds__(D) void merge_kernel(
-    eakvd_batch bt, int n_q, int max_chunks, int wpb, const float *__restrict__ part,
+    eakvd_batch bt, int n_q, int max_chunks, int wpb, int tt, const float *__restrict__ part,
     float *__restrict__ out)
 {
     const int qh = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
-    // blocks that had a tile (see mfma_kernel; wpb waves per block)
-    const int n_tiles = (bt.seq_len[s] + kTT - 1) / kTT;
+    // blocks that had a tile (see mfma_kernel; wpb waves per block, tt
+    // tokens per tile)
+    const int n_tiles = (bt.seq_len[s] + tt - 1) / tt;
     const int n_chunks = min(max_chunks, (n_tiles + wpb - 1) / wpb);
     const float *p = part + ((int64_t)s * n_q + qh) * max_chunks * (D + 2);
     // The (m, l) pair and o[i] of every chunk by vector buffer loads, all
@@ -1228,14 +1273,15 @@ constexpr int kPartBatch = 8;
 
 template <int D>
 __global__ __launch_bounds__(256) void merge_parts_kernel(
-    eakvd_batch bt, int n_q, int max_chunks, int wpb, const float *__restrict__ part,
+    eakvd_batch bt, int n_q, int max_chunks, int wpb, int tt, const float *__restrict__ part,
     float *__restrict__ out)
 {
     __shared__ float pm[kMergeParts], pl[kMergeParts], po[kMergeParts][32];
     const int qh = blockIdx.x / (D / 32), s = blockIdx.y;
     const int i = (blockIdx.x % (D / 32)) * 32 + (threadIdx.x & 31), pt = threadIdx.x >> 5;
-    // blocks that had a tile (see mfma_kernel; wpb waves per block)
-    const int n_tiles = (bt.seq_len[s] + kTT - 1) / kTT;
+    // blocks that had a tile (see mfma_kernel; wpb waves per block, tt
+    // tokens per tile)
+    const int n_tiles = (bt.seq_len[s] + tt - 1) / tt;
     const int n_chunks = min(max_chunks, (n_tiles + wpb - 1) / wpb);
     const float *p = part + ((int64_t)s * n_q + qh) * max_chunks * (D + 2);
     float M = -1000000.0f * EAKV_LOG2E, lt = 0.0f, ot = 0.0f;
@@ -1556,12 +1602,38 @@ int max_len(const eakvd_batch *b)
     return mx;
 }
 
+// Tokens per tile of the matrix-core program: 64 for two-quad waves that
+// each get at least kMinTiles64 tiles of 64, else 32.  Short contexts keep
+// the finer tiles, which give more waves work (32Q/4KV d64 at 4096 tokens:
+// 8.3 us per fused call with 32-token tiles, 9.7 with 64-token ones; 64Q/8KV
+// d128 at 131072 tokens: 38.9-39.0 against 39.5-39.6 us).
+constexpr int kMinTiles64 = 4;
+
+int tile_tokens(int hh, int ml, int mc, int wpb)
+{
+    const int64_t t64 = ((int64_t)ml + 63) / 64;
+    return hh == 2 && t64 >= (int64_t)kMinTiles64 * mc * wpb ? 64 : 32;
+}
+
+// The mfma_kernel instantiation of a launch shape
+template <bool VS>
+auto mfma_entry(int d, int hh, int tt)
+{
+    if (d == 64) {
+        if (hh == 1) return mfma_kernel<64, 1, VS, 32>;
+        return tt == 64 ? mfma_kernel<64, 2, VS, 64> : mfma_kernel<64, 2, VS, 32>;
+    }
+    if (hh == 1) return mfma_kernel<128, 1, VS, 32>;
+    return tt == 64 ? mfma_kernel<128, 2, VS, 64> : mfma_kernel<128, 2, VS, 32>;
+}
+
 // The launch shape of one fused call: the matrix-core program (chunks per
 // unit mc, waves per block wpb, virtual kv heads per kv head split, q heads
-// per virtual head qv, quads hh) or the VALU program (mc chunks of kChunkV).
+// per virtual head qv, quads hh, tokens per tile tt) or the VALU program
+// (mc chunks of kChunkV).
 struct FusedPlan {
     bool mfma;
-    int mc, wpb, split, qv, hh;
+    int mc, wpb, split, qv, hh, tt;
 };
 
 FusedPlan fused_plan(const eakvd_geom *g, const eakvd_batch *b, int n_q, int n_kv)
@@ -1582,6 +1654,7 @@ FusedPlan fused_plan(const eakvd_geom *g, const eakvd_batch *b, int n_q, int n_k
                                : (p.hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
         p.wpb = p.hh == 1 ? kWavesH<1> : kWavesH<2>;
         p.mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv * p.split, per_cu);
+        p.tt = tile_tokens(p.hh, ml, p.mc, p.wpb);
     } else {
         p.mc = (ml + kChunkV - 1) / kChunkV;
     }
@@ -1655,26 +1728,25 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         // more than one batch of chunks: the merge spread over 8 parts
         const bool parts = mc > kMergeBatch;
         const dim3 pgrid((unsigned)(n_q * (g->head_dim / 32)), (unsigned)b->n_seq);
-        auto kern = g->head_dim == 64
-                        ? (hh == 1 ? mfma_kernel<64, 1, false> : mfma_kernel<64, 2, false>)
-                        : (hh == 1 ? mfma_kernel<128, 1, false> : mfma_kernel<128, 2, false>);
+        auto kern = mfma_entry<false>(g->head_dim, hh, p.tt);
         const int64_t units = (int64_t)n_kv * p.split * b->n_seq;
         uint8_t *uc = merge_in_launch(g, ctr, mc, units) ? (uint8_t *)ctr : nullptr;
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, p.qv, rs,
                            part, p.split, out, uc);
         if (uc) return (int)hipGetLastError();
+        const int tt = p.tt;
         if (parts && g->head_dim == 64)
             hipLaunchKernelGGL(merge_parts_kernel<64>, pgrid, dim3(256), 0, st, *b, n_q, mc,
-                               wpb, part, out);
+                               wpb, tt, part, out);
         else if (parts)
             hipLaunchKernelGGL(merge_parts_kernel<128>, pgrid, dim3(256), 0, st, *b, n_q, mc,
-                               wpb, part, out);
+                               wpb, tt, part, out);
         else if (g->head_dim == 64)
             hipLaunchKernelGGL(merge_kernel<64>, mgrid, dim3(64), 0, st, *b, n_q, mc, wpb,
-                               part, out);
+                               tt, part, out);
         else
             hipLaunchKernelGGL(merge_kernel<128>, mgrid, dim3(128), 0, st, *b, n_q, mc, wpb,
-                               part, out);
+                               tt, part, out);
         return (int)hipGetLastError();
     }
     const int qpk = n_q / n_kv;
@@ -1733,11 +1805,10 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
                                          : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
     const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
     const int mc = mfma_blocks_per_unit(seq_len, n_kv * split, per_cu);
+    const int tt = tile_tokens(hh, seq_len, mc, wpb);
     const dim3 grid((unsigned)mc, (unsigned)(n_kv * split), 1u);
     float *part = (float *)work;
-    auto kern = g->head_dim == 64
-                    ? (hh == 1 ? mfma_kernel<64, 1, true> : mfma_kernel<64, 2, true>)
-                    : (hh == 1 ? mfma_kernel<128, 1, true> : mfma_kernel<128, 2, true>);
+    auto kern = mfma_entry<true>(g->head_dim, hh, tt);
     const int64_t units = (int64_t)n_kv * split;
     uint8_t *ctr = const_cast<uint8_t *>(base) + g->ctr_off;
     uint8_t *uc = merge_in_launch(g, ctr, mc, units) ? ctr : nullptr;
@@ -1745,7 +1816,7 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
                        part, split, out, uc);
     if (uc) return (int)hipGetLastError();
     // the chunks that hold a partial: blocks with a tile (see mfma_kernel)
-    const int n_tiles = (seq_len + kTT - 1) / kTT;
+    const int n_tiles = (seq_len + tt - 1) / tt;
     const int nch = min(mc, (n_tiles + wpb - 1) / wpb);
     if (g->head_dim == 64)
         hipLaunchKernelGGL(vsum_merge_kernel<64>, dim3((unsigned)(n_q * 2)), dim3(256), 0, st,

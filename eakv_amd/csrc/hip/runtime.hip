@@ -2,6 +2,8 @@
 // eakvd.h.  Every stream is created at the default priority.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "../eakvd.h"
 
 extern "C" {
@@ -25,17 +27,29 @@ int eakvd_host_malloc(void **p, size_t n)
 
 int eakvd_host_free(void *p) { return p ? (int)hipHostFree(p) : 0; }
 
-int eakvd_stream_create(void **s)
+// The caches' stream of a device: one per device, shared by every cache on
+// it, created at the first use and kept until the process ends.  Work of the
+// device's caches is then ordered by enqueue order alone, and batched calls
+// need no waits between the caches' streams.  (With a stream per cache, the
+// batched append of a decode step left a wait for its launch queued on every
+// other cache's stream, and while the host ran steps ahead those pending
+// waits slowed the fused calls already running: 8 caches of 32Q/8KV at
+// 32767 tokens, 59.5-60.3 against 56.6-57.0 us per call in steady state.)
+int eakvd_device_stream(int dev, void **s)
 {
-    hipStream_t st = nullptr;
-    hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
-    *s = (void *)st;
-    return (int)e;
-}
-
-int eakvd_stream_destroy(void *s)
-{
-    return s ? (int)hipStreamDestroy((hipStream_t)s) : 0;
+    static std::mutex mu;
+    static hipStream_t per_dev[64];
+    *s = nullptr;
+    if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!per_dev[dev]) {
+        hipStream_t st = nullptr;
+        hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+        if (e != hipSuccess) return (int)e;
+        per_dev[dev] = st;
+    }
+    *s = (void *)per_dev[dev];
+    return 0;
 }
 
 int eakvd_stream_sync(void *s) { return (int)hipStreamSynchronize((hipStream_t)s); }

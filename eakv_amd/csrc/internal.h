@@ -22,7 +22,8 @@ struct eakv_cache {
     int        device;     /* HIP ordinal current at creation */
     uint8_t   *dev;        /* planes */
     size_t     dev_bytes;
-    void      *stream;     /* default-priority, non-blocking */
+    void      *stream;     /* the device's caches' stream (eakvd_device_stream):
+                              default priority, non-blocking, shared */
 
     void  *work;           /* device scratch for staging and partials */
     size_t work_bytes;

@@ -4,7 +4,10 @@
  * memory.  They exist because the reference API takes host pointers, which
  * forces a PCIe round trip per call on a GPU:
  *   - device-pointer forms of load/append/scores/output, asynchronous on a
- *     HIP stream (pass the hipStream_t as void*, NULL = the cache's own);
+ *     HIP stream (pass the hipStream_t as void*, NULL = the cache's own:
+ *     one non-blocking stream per device, shared by every cache created on
+ *     that device, so the device's caches' default-stream work runs in
+ *     enqueue order);
  *   - batched append and batched fused decode attention over several caches
  *     of the same shape (one launch per layer for all sequences);
  *   - the fused single-pass softmax attention, which the reference compiles
@@ -41,8 +44,9 @@ int         eakv_last_error(void);
 const char *eakv_last_error_message(void);
 void        eakv_clear_error(void);
 
-/* The HIP device ordinal the cache lives on, its stream, and a wait for all
- * work enqueued on that stream. */
+/* The HIP device ordinal the cache lives on, its stream (the device's
+ * caches' shared stream), and a wait for all work enqueued on that stream
+ * (by any cache of the device). */
 int   eakv_cache_device(const eakv_cache_t *cache);
 void *eakv_cache_stream(const eakv_cache_t *cache);
 int   eakv_cache_sync(const eakv_cache_t *cache);

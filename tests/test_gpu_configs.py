@@ -298,6 +298,59 @@ def test_blocks_beyond_1gib(E, rng, nkv, n_q, d, lmax, L):
 
 # -------------------------------------------- long contexts: 8-part merge
 
+def tile_tokens(L, units, qpk, d):
+    """Tokens per tile of the fused matrix-core program (fused.hip's
+    tile_tokens): 64 where waves serve two quads (5-8 q heads per kv head)
+    and each of the unit's 8 waves per chunk gets at least 4 tiles of 64,
+    else 32."""
+    mc = mfma_chunks(L, units, qpk, d)
+    return 64 if qpk > 4 and -(-L // 64) >= 4 * mc * 8 else 32
+
+
+# ------------------------------------------ 64-token tiles (two-quad waves)
+
+@pytest.mark.parametrize("d,n_q,n_kv,L,case", [
+    (128, 64, 8, 65536 + 37, "random"), (128, 48, 8, 70000, "nan-v"),
+    (128, 64, 8, 66000, "slope"), (64, 128, 16, 65600, "random")])
+def test_64_token_tiles(E, rng, d, n_q, n_kv, L, case):
+    """Long contexts at 6-8 q heads per kv head run 64-token tiles (one
+    16x16x64 V product and one recombination per 64 tokens).  Fused
+    attention against the oracle with a ragged last tile, a NaN V value,
+    scores that rise along the context (the running max moves), and the
+    V-sum mode with signed weights (the V-sum's grid has the same chunks,
+    so it runs 64-token tiles too)."""
+    assert tile_tokens(L, n_kv, n_q // n_kv, d) == 64
+    say("tt64", d, n_q, n_kv, L, case)
+    if case == "slope":
+        u = rng.standard_normal((n_kv, d))
+        u /= np.linalg.norm(u, axis=1, keepdims=True)
+        t = np.arange(L, dtype=np.float64) - L / 2
+        K = (0.0015 * t)[None, :, None] * u[:, None, :] + 0.1 * rng.standard_normal((n_kv, L, d))
+        data = np.stack([K, rng.standard_normal((n_kv, L, d))])[None].astype(np.float32)
+        q = (np.repeat(u, n_q // n_kv, axis=0) * np.sqrt(d) +
+             0.3 * rng.standard_normal((n_q, d))).astype(np.float32)
+    else:
+        data = rng.standard_normal((1, 2, n_kv, L, d)).astype(np.float32)
+        q = rng.standard_normal((n_q, d)).astype(np.float32)
+    if case == "nan-v":
+        # the first value of a group (the quantizer's scan carries a NaN
+        # only from there): that group's 64 dims of kv head 3 turn NaN
+        data[0, 1, 3, L - 5, 64] = np.nan
+    g, o = pair(E, 1, n_kv, d, L + 8)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    a = g.attention_fused(q, 0, n_q, n_kv)
+    b = o.attention_fused(q, 0, n_q, n_kv)
+    nan = np.isnan(b)
+    assert nan.any() == (case == "nan-v")
+    assert np.array_equal(np.isnan(a), nan)
+    ok, err, nbad = tol_close(a[~nan], b[~nan], ATOL, RTOL)
+    assert ok, (err, nbad)
+    if case == "random":
+        unfused_check(g, o, q, 0, n_q, n_kv, rng, signed=True)
+    g.free()
+
+
 @pytest.mark.parametrize("d,n_q,n_kv,L,where", [(128, 8, 2, 8192, "k"), (128, 16, 2, 4600, "v"),
                                                 (64, 8, 2, 6000, "v")])
 def test_long_context_nonfinite_values(E, rng, d, n_q, n_kv, L, where):

@@ -23,7 +23,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "eakv_amd")
 ASM = os.path.join(PKG, "_build", "fused_gfx950.s")
-NAME = re.compile(r"^(_ZN12_GLOBAL__N_111mfma_kernelILi(\d+)ELi(\d)ELb(\d)E\S*):")
+NAME = re.compile(r"^(_ZN12_GLOBAL__N_111mfma_kernelILi(\d+)ELi(\d)ELb(\d)ELi(\d+)E\S*):")
 
 
 @pytest.fixture(scope="module")
@@ -42,8 +42,8 @@ def kernels():
         j = i + 1
         while not lines[j].startswith(".Lfunc_end"):
             j += 1
-        d, hh, vs = int(m.group(2)), int(m.group(3)), m.group(4) == "1"
-        out[(d, hh, vs)] = lines[i + 1:j]
+        d, hh, vs, tt = int(m.group(2)), int(m.group(3)), m.group(4) == "1", int(m.group(5))
+        out[(d, hh, vs, tt)] = lines[i + 1:j]
         i = j
     return out
 
@@ -64,18 +64,22 @@ def blocks(body):
     return res
 
 
+INSTANCES = [(d, hh, vs, tt) for d in (64, 128) for hh in (1, 2) for vs in (False, True)
+             for tt in ((32,) if hh == 1 else (32, 64))]
+
+
 def test_every_instantiation_found(kernels):
-    assert set(kernels) == {(d, hh, vs) for d in (64, 128) for hh in (1, 2)
-                            for vs in (False, True)}
+    assert set(kernels) == set(INSTANCES)
 
 
-@pytest.mark.parametrize("d,hh,vs", [(d, hh, vs) for d in (64, 128) for hh in (1, 2)
-                                     for vs in (False, True)])
-def test_groups_issued_in_source_order(kernels, d, hh, vs):
-    n_lds = (32 * (d // 2)) // 1024 + 1          # V loads (1 KB each) + the scale load
-    n_reg = 2 * hh if vs else 2 * (d // 64)      # weights, or K bytes (16-token halves x groups)
+@pytest.mark.parametrize("d,hh,vs,tt", INSTANCES)
+def test_groups_issued_in_source_order(kernels, d, hh, vs, tt):
+    gpd = d // 64
+    n_scale = max(4 * tt * gpd * 4, 1024) // 1024  # scale loads (1 KB each)
+    n_lds = (tt * 32 * gpd) // 1024 + n_scale    # V loads (1 KB each) + the scale loads
+    n_reg = (tt // 16) * (hh if vs else gpd)     # weights, or K bytes (16-token parts x groups)
     group = "D" * n_lds + "g" * n_reg
-    with_loads = [(lb, tk) for lb, tk in blocks(kernels[(d, hh, vs)]) if tk]
+    with_loads = [(lb, tk) for lb, tk in blocks(kernels[(d, hh, vs, tt)]) if tk]
     assert with_loads, "no pipeline loads found"
     # prologue: the 4-byte prime load of a V slot and the first scale load
     # come first (the first explicit wait needs exactly those two)
