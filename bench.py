@@ -92,6 +92,21 @@ class Synth:
         self.lib.eakv_synth_softmax.restype = C.c_int
         self.lib.eakv_synth_softmax.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                                                 C.c_void_p]
+        self.lib.eakv_synth_hold.restype = C.c_int
+        self.lib.eakv_synth_hold.argtypes = [C.c_int, C.c_void_p]
+
+    _one = None
+
+    @classmethod
+    def get(cls):
+        if cls._one is None:
+            cls._one = cls()
+        return cls._one
+
+    def hold(self, us, stream=None):
+        rc = self.lib.eakv_synth_hold(int(us), stream)
+        if rc:
+            raise RuntimeError(f"hold launch failed: {rc}")
 
     def fill(self, ptr, n_rows, n_tok, d, seed, row0, pos0, kind, chan_ptr=None,
              stream=None):
@@ -260,19 +275,42 @@ class Workload:
         return ks, sm, vs
 
 
-def timed(H, stream, fn, steps, warmup, per):
+def timed(H, stream, fn, steps, warmup, per, queued=False):
     """Mean µs per unit of `fn` (one call = `per` units) between two events
-    on `stream`, after `warmup` untimed calls."""
+    on `stream`, after `warmup` untimed calls.
+
+    queued: the timed calls are enqueued behind a hold launch (one sleeping
+    wave) that outlasts their issue on the host, so they run back to back
+    from a full queue: device time per call, without the host's issue rate.
+    A call of a few microseconds is otherwise host-bound (a 3.4 us K-score
+    launch issued from Python every 3.5-8.5 us).  Returns (µs, host issue µs
+    per unit) in that mode; the hold is doubled and the run repeated while
+    the issue outlasts it."""
+    t0 = time.perf_counter()
     for _ in range(warmup):
         fn()
+    host = (time.perf_counter() - t0) / max(1, warmup)
     H.synchronize()
-    e0, e1 = H.Event(), H.Event()
-    e0.record(stream)
-    for _ in range(steps):
-        fn()
-    e1.record(stream)
-    e1.synchronize()
-    return e0.elapsed_ms(e1) * 1e3 / (steps * per)
+    hold_us = int(host * 1e6 * steps * 2) + 500
+    for _ in range(4 if queued else 1):
+        e0, e1 = H.Event(), H.Event()
+        if queued:
+            Synth.get().hold(hold_us, stream)
+        e0.record(stream)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        issue_us = (time.perf_counter() - t0) * 1e6
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (steps * per)
+        if not queued:
+            return us
+        if issue_us < 0.8 * hold_us:
+            return us, issue_us / (steps * per)
+        hold_us *= 2
+    raise RuntimeError(f"timed: the host issue ({issue_us:.0f} us) outlasted a "
+                       f"{hold_us // 2} us hold")
 
 
 # ---------------------------------------------------------------- CPU side
@@ -435,7 +473,10 @@ def measure_unfused(w, steps, warmup):
     """The reference API's unfused step on the first cache, every layer:
     eakv_attention_scores_device, the caller's row softmax, then
     eakv_attention_output_device.  Per-call means of each phase (all layers
-    back to back, one event pair) and of the whole step."""
+    back to back, one event pair) and of the whole step, enqueued behind a
+    hold so that they run from a full queue; and the whole step as issued by
+    this Python loop straight onto an idle device (host-bound for short
+    calls)."""
     E, H, c = w.E, w.H, w.cfg
     cache = w.caches[0]
     L, nq, nkv, d = w.L0, c["nq"], c["nkv"], c["d"]
@@ -466,8 +507,11 @@ def measure_unfused(w, steps, warmup):
             assert lib.eakv_attention_output_device(cache.h, wts.ptr, l, nq, nkv, out.ptr,
                                                     None) == 0, E.last_error()
 
-    res = {name: timed(H, w.stream, fn, steps, warmup, c["nl"])
-           for name, fn in (("k_score", ks), ("softmax", sm), ("v_sum", vs), ("step", whole))}
+    res, issue = {}, {}
+    for name, fn in (("k_score", ks), ("softmax", sm), ("v_sum", vs), ("step", whole)):
+        res[name], issue[name] = timed(H, w.stream, fn, steps, warmup, c["nl"], queued=True)
+    res["host_issue_us"] = issue
+    res["step_host_issued"] = timed(H, w.stream, whole, steps, warmup, c["nl"])
     for a in (scores, wts, out):
         a.free()
     return res
@@ -483,7 +527,7 @@ def fused_call_us(w, steps, warmup):
             assert E.lib().eakv_attention_fused_batch_device(
                 w.handles, c["nseq"], l, w.ql[l].ptr, c["nq"], c["nkv"], w.out.ptr,
                 None) == 0, E.last_error()
-    return timed(H, w.stream, run, steps, warmup, c["nl"])
+    return timed(H, w.stream, run, steps, warmup, c["nl"], queued=True)[0]
 
 
 def read_peak(n_bytes, regions=8, reps=3, per_cu=3):
@@ -568,6 +612,11 @@ def run_config(cid, steps, warmup, ctx=None, with_cpu=True, log=print):
             "gbs": round(gbs(alg, u["step"]), 1), "frac": round(gbs(alg, u["step"]) / HBM_PEAK_GBS, 4),
             "alg_bytes_per_layer_step": alg,
             "kernels_us_per_layer": {k: round(u[k], 3) for k in ("k_score", "softmax", "v_sum")},
+            "timing": "device time of calls enqueued behind a hold (run back to back from "
+                      "a full queue); host_issued_us_per_layer_step: the same step issued "
+                      "from Python onto an idle device",
+            "host_issued_us_per_layer_step": round(u["step_host_issued"], 3),
+            "host_issue_us_per_call": {k: round(v, 3) for k, v in u["host_issue_us"].items()},
             "k_score_gbs": round(gbs(ks_b, u["k_score"]), 1),
             "v_sum_gbs": round(gbs(vs_b, u["v_sum"]), 1),
             "fused_call_us_per_layer": round(fz, 3),

@@ -232,3 +232,40 @@ extern "C" int eakv_synth_copy(void *dst, const void *src, int64_t n_bytes,
                        (hipStream_t)stream, (uint4 *)dst, (const uint4 *)src, n16);
     return (int)hipGetLastError();
 }
+
+namespace {
+
+// One wave sleeps until the device's real-time counter has advanced `ticks`
+// past its first reading, or after `max_iter` sleeps, whichever comes
+// first: every launch ends.
+__global__ __launch_bounds__(64) void hold_kernel(uint64_t ticks, int max_iter)
+{
+    const uint64_t t0 = wall_clock64();
+    for (int i = 0; i < max_iter; i++) {
+        if (wall_clock64() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(64);
+    }
+}
+
+}  // namespace
+
+// Occupies `stream` for about `us` microseconds (at most 100 ms) with one
+// sleeping wave, so that the calls the host enqueues behind it wait in the
+// stream's queue and then run back to back: the device time of a run of short
+// calls without the host's issue rate in it.
+extern "C" int eakv_synth_hold(int us, void *stream)
+{
+    if (us <= 0) return 0;
+    if (us > 100000) us = 100000;
+    // s_sleep 64 is about 64 x 64 clocks, 1.7-4 us; the cap ends the launch
+    // within a few times the request even if the counter does not advance.
+    const int max_iter = us + 1000;
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
+        khz <= 0)
+        khz = 100000;
+    hipLaunchKernelGGL(hold_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                       (uint64_t)us * (uint64_t)khz / 1000, max_iter);
+    return (int)hipGetLastError();
+}
