@@ -89,18 +89,24 @@ __global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst,
         dst[i] = src[i];
 }
 
-// Plain streaming read, two 16-byte loads in flight per lane, the words
-// xor-folded into one word per thread: the device's sustained read rate for
-// one contiguous region, the practical ceiling of a bandwidth-bound pass.
+// Plain streaming read, two 16-byte non-temporal loads in flight per lane,
+// the words xor-folded into one word per thread: the device's sustained read
+// rate for one contiguous region, the practical ceiling of a bandwidth-bound
+// pass.  The non-temporal hint is worth about 7% (335.8 MB passes, 3 blocks
+// per CU: 6.78-6.80 against 6.29-6.39 TB/s), as on the fused kernel's plane
+// loads.
 __global__ __launch_bounds__(256) void read_kernel(const uint4 *__restrict__ src, int64_t n16,
                                                    unsigned *__restrict__ sink)
 {
     const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t nt = (int64_t)gridDim.x * 256;
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src);
     unsigned a = 0;
     for (int64_t i = tid; i < n16; i += 2 * nt) {
-        const uint4 u = src[i];
-        const uint4 v = i + nt < n16 ? src[i + nt] : uint4{0, 0, 0, 0};
+        const u32x4 u = __builtin_nontemporal_load(&s4[i]);
+        const u32x4 v = i + nt < n16 ? __builtin_nontemporal_load(&s4[i + nt])
+                                     : u32x4{0, 0, 0, 0};
         a ^= u.x ^ u.y ^ u.z ^ u.w ^ v.x ^ v.y ^ v.z ^ v.w;
     }
     sink[tid] = a;
