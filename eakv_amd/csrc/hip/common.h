@@ -59,6 +59,13 @@ __device__ __forceinline__ float ld_dev(const float *p)
 {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// two adjacent floats (8-byte aligned) in one device-scope load
+__device__ __forceinline__ float2 ld_dev2(const float *p)
+{
+    const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(p)),
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
 
 // Reference reduce_add over 16 lanes, pairwise halving tree (the order the
 // CPU restatement fixes): v8[i]=a[i]+a[i+8], v4, v2, then v2[0]+v2[1].

@@ -430,76 +430,131 @@ struct WaveState {
     float lsum, m;
 };
 
-// The chunk merges of a launch that merges its own chunks (at most
-// kInBatch chunks per unit): the partials of one (sequence, q head) at p,
-// n_chunks of them, read with device-scope loads all issued at once (one
-// round trip).  Each thread restates, for its output i, the arithmetic of
-// the merge launch the same call would make, in the same order, so both
-// give the same bits: merge_kernel, and vsum_merge_kernel in V-sum mode.
+// The chunk merge of a launch that merges its own chunks (at most kInBatch
+// chunks per unit), done by the block of the unit that counts last.  Each
+// thread restates, for its two adjacent outputs, the arithmetic of the merge
+// launch the same call would make, in the same order, so both give the same
+// bits: merge_kernel, and vsum_merge_kernel in V-sum mode.  Loads: the (m, l)
+// pair of every (head, chunk) once per block into LDS (one 8-byte
+// device-scope load each), and per thread the o pairs of kInBatch chunks
+// (one 8-byte device-scope load each), all issued before the barrier: one
+// round trip.
+// (A first form had every thread load m, l and o of kInBatch clamped chunks
+// for each of its outputs, 96 loads per thread; its merge cost about 3 us of
+// an 8 x 32Q/8KV call at 32767 tokens.)
 constexpr int kInBatch = 16;    // merge_kernel's batch
 constexpr int kInParts = 8;     // vsum_merge_kernel's parts
 
-// Softmax merge: M = max(-1e6 log2(e), m_c), l = sum l_c 2^(m_c - M),
-// o = sum o_c 2^(m_c - M), out = o * (1/l).
-template <int D>
-__device__ __forceinline__ float merge_chunks(const float *p, int n_chunks, int i)
+// pu: the partials of the unit's first q head (head h, chunk c at
+// (h * nb + c) * (D + 2): m, l, o[D]); stage: LDS, 2 * kInBatch floats per
+// head; G q heads; outputs ou[G][D]; P adjacent outputs per thread (1 where
+// G * D <= nthreads, else 2).  Every thread of the block calls it (it holds
+// a barrier).
+template <int D, bool VS, int P>
+__device__ __forceinline__ void merge_unit_p(const float *pu, int nb, int n_chunks, int G,
+                                             float *stage, float *ou, int tid)
 {
-    float m[kInBatch], lv[kInBatch], ov[kInBatch];
+    const bool has = P * tid < G * D;
+    const int h = has ? P * tid / D : 0, dim = P * tid % D;
+    const float *ph = pu + (int64_t)h * nb * (D + 2) + 2 + dim;
+    // the (m, l) pair of (head, chunk) k = tid (G * n_chunks <= nthreads),
+    // then the o values: unconditional, clamped to the last chunk, no branch
+    // between the loads (entries past the last chunk hold its values); the
+    // pair goes to LDS once its load is in, the o loads still in flight
+    const bool stg = tid < G * n_chunks;
+    const int sh = stg ? tid / n_chunks : 0, sc = stg ? tid % n_chunks : 0;
+    const float2 ml = ld_dev2(pu + ((int64_t)sh * nb + sc) * (D + 2));
+    float ov[kInBatch][P];
 #pragma unroll
     for (int j = 0; j < kInBatch; j++) {
-        const float *pc = p + min(j, n_chunks - 1) * (D + 2);
-        m[j] = ld_dev(pc);
-        lv[j] = ld_dev(pc + 1);
-        ov[j] = ld_dev(pc + 2 + i);
-    }
-    const float M = -1000000.0f * EAKV_LOG2E;
-    float Mn = M, lt = 0.0f, ot = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kInBatch; j++)
-        if (j < n_chunks) Mn = fmaxf(Mn, m[j]);
-    const float f = __builtin_amdgcn_exp2f(M - Mn);
-    lt *= f;
-    ot *= f;
-#pragma unroll
-    for (int j = 0; j < kInBatch; j++) {
-        const float wj = j < n_chunks ? __builtin_amdgcn_exp2f(m[j] - Mn) : 0.0f;
-        lt = fmaf(lv[j], wj, lt);
-        ot = fmaf(ov[j], wj, ot);
-    }
-    return ot * (1.0f / lt);
-}
-
-// V-sum mode: the plain sum of o_c in 8 strided parts (chunks pt, pt + 8)
-// added in part order, NaN when a chunk's l is NaN (a non-finite weight).
-template <int D>
-__device__ __forceinline__ float vs_chunk_sum(const float *p, int n_chunks, int i)
-{
-    float o[kInBatch], l[kInBatch];
-#pragma unroll
-    for (int j = 0; j < kInBatch; j++) {
-        const float *pc = p + min(j, n_chunks - 1) * (D + 2);
-        l[j] = ld_dev(pc + 1);
-        o[j] = ld_dev(pc + 2 + i);
-    }
-    float t = 0.0f, fl = 0.0f;
-#pragma unroll
-    for (int pt = 0; pt < kInParts; pt++) {
-        float sum = 0.0f, bad = 0.0f;
-#pragma unroll
-        for (int c = pt; c < kInBatch; c += kInParts)
-            if (c < n_chunks) {
-                sum = __fadd_rn(sum, o[c]);
-                bad = bad + l[c];                 // 0, or NaN after a non-finite weight
-            }
-        if (pt == 0) {
-            t = sum;
-            fl = bad;
+        const float *pj = ph + min(j, n_chunks - 1) * (D + 2);
+        if constexpr (P == 2) {
+            const float2 v = ld_dev2(pj);
+            ov[j][0] = v.x;
+            ov[j][1] = v.y;
         } else {
-            t = __fadd_rn(t, sum);
-            fl = fl + bad;
+            ov[j][0] = ld_dev(pj);
         }
     }
-    return fl == fl ? t : fl;
+    if (stg) {
+        stage[sh * 2 * kInBatch + sc] = ml.x;
+        stage[sh * 2 * kInBatch + kInBatch + sc] = ml.y;
+    }
+    __syncthreads();
+    if (!has) return;
+    // every staged (m, l) of the head into registers at once (16-byte LDS
+    // reads; entries past the last chunk are not used or are replaced by
+    // the last chunk's l), so the selects below need no LDS round trips
+    const float4 *m4 = reinterpret_cast<const float4 *>(stage + h * 2 * kInBatch);
+    float mv[kInBatch], lv[kInBatch];
+#pragma unroll
+    for (int q = 0; q < kInBatch / 4; q++) {
+        const float4 a = m4[q], b = m4[kInBatch / 4 + q];
+        mv[4 * q] = a.x; mv[4 * q + 1] = a.y; mv[4 * q + 2] = a.z; mv[4 * q + 3] = a.w;
+        lv[4 * q] = b.x; lv[4 * q + 1] = b.y; lv[4 * q + 2] = b.z; lv[4 * q + 3] = b.w;
+    }
+    float r[P];
+    if constexpr (!VS) {
+        // softmax merge: M = max(-1e6 log2(e), m_c), l = sum l_c 2^(m_c - M),
+        // o = sum o_c 2^(m_c - M), out = o * (1/l); the batch's entries past
+        // the last chunk repeat the last chunk's l and o with weight 0
+        const float M = -1000000.0f * EAKV_LOG2E;
+        float Mn = M, lt = 0.0f, o[P];
+#pragma unroll
+        for (int e = 0; e < P; e++) o[e] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kInBatch; j++) Mn = j < n_chunks ? fmaxf(Mn, mv[j]) : Mn;
+        const float f = __builtin_amdgcn_exp2f(M - Mn);
+        lt *= f;
+#pragma unroll
+        for (int e = 0; e < P; e++) o[e] *= f;
+        const float llast = stage[h * 2 * kInBatch + kInBatch + n_chunks - 1];
+#pragma unroll
+        for (int j = 0; j < kInBatch; j++) {
+            const bool in = j < n_chunks;
+            const float wj = in ? __builtin_amdgcn_exp2f(mv[j] - Mn) : 0.0f;
+            lt = fmaf(in ? lv[j] : llast, wj, lt);
+#pragma unroll
+            for (int e = 0; e < P; e++) o[e] = fmaf(ov[j][e], wj, o[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < P; e++) r[e] = o[e] * (1.0f / lt);
+    } else {
+        // V-sum: the plain sum of o_c in 8 strided parts (chunks pt, pt + 8)
+        // added in part order, NaN when a chunk's l is NaN (a non-finite
+        // weight)
+        float t[P], fl = 0.0f;
+#pragma unroll
+        for (int e = 0; e < P; e++) t[e] = 0.0f;
+#pragma unroll
+        for (int pt = 0; pt < kInParts; pt++) {
+            float sm[P], bad = 0.0f;
+#pragma unroll
+            for (int e = 0; e < P; e++) sm[e] = 0.0f;
+#pragma unroll
+            for (int c = pt; c < kInBatch; c += kInParts) {
+                const bool in = c < n_chunks;
+#pragma unroll
+                for (int e = 0; e < P; e++) sm[e] = in ? __fadd_rn(sm[e], ov[c][e]) : sm[e];
+                bad = in ? bad + lv[c] : bad;     // 0, or NaN after a non-finite weight
+            }
+#pragma unroll
+            for (int e = 0; e < P; e++) t[e] = pt == 0 ? sm[e] : __fadd_rn(t[e], sm[e]);
+            fl = pt == 0 ? bad : fl + bad;
+        }
+#pragma unroll
+        for (int e = 0; e < P; e++) r[e] = fl == fl ? t[e] : fl;
+    }
+#pragma unroll
+    for (int e = 0; e < P; e++) ou[h * D + dim + e] = r[e];
+}
+
+template <int D, bool VS>
+__device__ __forceinline__ void merge_unit(const float *pu, int nb, int n_chunks, int G,
+                                           float *stage, float *ou, int tid, int nthreads)
+{
+    if (G * D <= nthreads) merge_unit_p<D, VS, 1>(pu, nb, n_chunks, G, stage, ou, tid);
+    else merge_unit_p<D, VS, 2>(pu, nb, n_chunks, G, stage, ou, tid);
 }
 
 // Tile assignment: nb = gridDim.x blocks share one (sequence, kv head), a
@@ -1200,13 +1255,11 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     __syncthreads();
     if (((const int *)z_lds[0])[0] == 0) return;
     if (tid == 0) __hip_atomic_store(uc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int i = tid; i < G * D; i += 64 * NW) {
-        const int h = i / D, dim = i % D;
-        const int64_t qh = (int64_t)s * n_q + kvh * qpk + h;
-        const float *pq = part + qh * nb * (D + 2);
-        out[qh * D + dim] = VS ? vs_chunk_sum<D>(pq, n_chunks, dim)
-                               : merge_chunks<D>(pq, n_chunks, dim);
-    }
+    static_assert(4 * HH * D / 2 <= 64 * NW && 4 * HH * kInBatch <= 64 * NW,
+                  "one output pair and at most one (m, l) pair per thread");
+    const int64_t qh0 = (int64_t)s * n_q + kvh * qpk;
+    merge_unit<D, VS>(part + qh0 * nb * (D + 2), nb, n_chunks, G, &s_lds0[0][0],
+                      out + qh0 * D, tid, 64 * NW);
 }
 
 // Merge of the MFMA program's chunk partials (log2 domain) per (q head,
