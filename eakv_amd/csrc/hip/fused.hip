@@ -95,7 +95,10 @@ constexpr int kSlots = EAKV_FUSED_SLOTS;
 #ifndef EAKV_SHARE_Q
 #define EAKV_SHARE_Q 1
 #endif
-constexpr bool kShareQ = EAKV_SHARE_Q;    // one wave per quad computes the q operands
+constexpr bool kShareQ = EAKV_SHARE_Q;
+#ifndef EAKV_OOB_TAIL
+#define EAKV_OOB_TAIL 1
+#endif    // one wave per quad computes the q operands
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void *lds_ptr;
@@ -198,7 +201,7 @@ __device__ __forceinline__ uint2 ldb64(__amdgpu_buffer_rsrc_t r, uint32_t vo, ui
 // weight is exactly 0.  dt is the same in every lane; readfirstlane makes
 // that visible, so the tile offset goes to the scalar soffset operand.
 template <int D, int TT>
-__device__ __forceinline__ void load_k(Stage<D, TT> &T, const LaneOffs &P, int dt)
+__device__ __forceinline__ void load_k(Stage<D, TT> &T, const LaneOffs &P, int dt, uint32_t ob)
 {
     constexpr int GPD = D / 64;
     const uint32_t ws = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 32;
@@ -206,7 +209,7 @@ __device__ __forceinline__ void load_k(Stage<D, TT> &T, const LaneOffs &P, int d
     for (int k = 0; k < Geo<D, TT>::NK; k++)
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
-            T.kw[k][gg] = ldb64(P.kw, P.kwo, ws + (16 * k * GPD + gg) * 32);
+            T.kw[k][gg] = ldb64(P.kw, P.kwo + ob, ws + (16 * k * GPD + gg) * 32);
 }
 
 // V-sum mode: the weights of the tile at token offset dt, w[head][dt + 16k +
@@ -231,14 +234,15 @@ __device__ __forceinline__ void load_w(WStage<D, HH, TT> &T, __amdgpu_buffer_rsr
 // load to LDS: lane m's 16 bytes land at the instruction's LDS start + 16m;
 // the lane fetches the unit that belongs there, see LaneOffs.vwo).
 template <int D, int TT>
-__device__ __forceinline__ void load_v(uint8_t *vslot, const LaneOffs &P, int dt)
+__device__ __forceinline__ void load_v(uint8_t *vslot, const LaneOffs &P, int dt, uint32_t ob)
 {
     constexpr int GPD = D / 64;
     const uint32_t ws = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 32;
 #pragma unroll
     for (int i = 0; i < Geo<D, TT>::NVD; i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(P.vw, (lds_ptr)(vslot + 1024 * i), 16,
-                                                 (int)P.vwo, (int)(ws + 1024 * i), 0, kPlaneAux);
+                                                 (int)(P.vwo + ob), (int)(ws + 1024 * i), 0,
+                                                 kPlaneAux);
 }
 
 // The K and V scales and biases of the tile at dt into a scale slot, NSL
@@ -248,14 +252,14 @@ __device__ __forceinline__ void load_v(uint8_t *vslot, const LaneOffs &P, int dt
 // (instruction i, lane m: plane (64i + m) / LP; at d=64 with 32-token tiles
 // lanes 32-63 repeat lanes 0-31 into the unused second half of the slot).
 template <int D, int TT>
-__device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int dt)
+__device__ __forceinline__ void load_scales(float *slot, const LaneOffs &P, int dt, uint32_t ob)
 {
     constexpr int GPD = D / 64;
     const uint32_t ss = (uint32_t)__builtin_amdgcn_readfirstlane(dt) * GPD * 4;
 #pragma unroll
     for (int i = 0; i < Geo<D, TT>::NSL; i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(P.layer, (lds_ptr)(slot + 256 * i), 16,
-                                                 (int)P.sco[i], (int)ss, 0, kPlaneAux);
+                                                 (int)(P.sco[i] + ob), (int)ss, 0, kPlaneAux);
 }
 
 // Loads per group, in issue order: V chunks, scales, then the K bytes (or
@@ -756,18 +760,24 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // token offset of a tile for loads: past-the-end tiles re-read the
     // unit's last tile (in bounds; their scores are masked)
     auto ldt = [&](int t) { return min(t, n_tiles - 1) * TT; };
+    // Past-the-end tiles are also read out of range (a lane offset beyond
+    // every plane: the loads return 0 at once, with no memory request), so
+    // a wave's last groups, never consumed except as masked tokens, do not
+    // hold up its epilogue.  The tile offset stays clamped in range.
+    auto oob = [&](int t) -> uint32_t { return EAKV_OOB_TAIL && t >= n_tiles ? 0x80000000u : 0u; };
 
     StageT st[kSlots];
     // group j: V of tile T(j-1) into V slot (j-1) % kSlots, then the scales
     // and K bytes of tile T(j) into scale slot and stage j % kSlots
     auto load_group = [&](auto jc, int tv, int tkk) {
         constexpr int j = decltype(jc)::value;
-        load_v<D, TT>(vslot(std::integral_constant<int, (j + kSlots - 1) % kSlots>{}), P, ldt(tv));
+        load_v<D, TT>(vslot(std::integral_constant<int, (j + kSlots - 1) % kSlots>{}), P, ldt(tv),
+                      oob(tv));
         __builtin_amdgcn_sched_barrier(0);
-        load_scales<D, TT>(sslot(std::integral_constant<int, j % kSlots>{}), P, ldt(tkk));
+        load_scales<D, TT>(sslot(std::integral_constant<int, j % kSlots>{}), P, ldt(tkk), oob(tkk));
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (VS) load_w<D, HH, TT>(st[j % kSlots], wr, wo, ldt(tkk), tl, L);
-        else load_k<D, TT>(st[j % kSlots], P, ldt(tkk));
+        else load_k<D, TT>(st[j % kSlots], P, ldt(tkk), oob(tkk));
         __builtin_amdgcn_sched_barrier(0);
     };
     // Unconditional (a wave without tiles reads the unit's last tile), so
@@ -778,13 +788,14 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // in the loop's order, which keeps the compiler's wait placement at the
     // loop head as tight as inside the loop.
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        P.vw, (lds_ptr)vslot(std::integral_constant<int, kSlots - 1>{}), 4, (int)P.vwo,
+        P.vw, (lds_ptr)vslot(std::integral_constant<int, kSlots - 1>{}), 4,
+        (int)(P.vwo + oob(tk[0])),
         (int)((uint32_t)__builtin_amdgcn_readfirstlane(ldt(tk[0])) * GPD * 32), 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    load_scales<D, TT>(sslot(I0{}), P, ldt(tk[0]));
+    load_scales<D, TT>(sslot(I0{}), P, ldt(tk[0]), oob(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (VS) load_w<D, HH, TT>(st[0], wr, wo, ldt(tk[0]), tl, L);
-    else load_k<D, TT>(st[0], P, ldt(tk[0]));
+    else load_k<D, TT>(st[0], P, ldt(tk[0]), oob(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
     load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
     if constexpr (kSlots > 2) load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
