@@ -436,13 +436,13 @@ struct WaveState {
 
 // The chunk merge of a launch that merges its own chunks (at most kInBatch
 // chunks per unit), done by the block of the unit that counts last.  Each
-// thread restates, for its two adjacent outputs, the arithmetic of the merge
-// launch the same call would make, in the same order, so both give the same
-// bits: merge_kernel, and vsum_merge_kernel in V-sum mode.  Loads: the (m, l)
-// pair of every (head, chunk) once per block into LDS (one 8-byte
-// device-scope load each), and per thread the o pairs of kInBatch chunks
-// (one 8-byte device-scope load each), all issued before the barrier: one
-// round trip.
+// thread restates, for its one or two adjacent outputs, the arithmetic of
+// the merge launch the same call would make, in the same order, so both give
+// the same bits: merge_kernel, and vsum_merge_kernel in V-sum mode.  Loads:
+// the (m, l) pair of every (head, chunk) once per block into LDS (one 8-byte
+// device-scope load each), and per thread the o values of kInBatch chunks
+// (one 4- or 8-byte device-scope load each), all issued before the barrier:
+// one round trip.
 // (A first form had every thread load m, l and o of kInBatch clamped chunks
 // for each of its outputs, 96 loads per thread; its merge cost about 3 us of
 // an 8 x 32Q/8KV call at 32767 tokens.)
