@@ -59,6 +59,13 @@ __device__ __forceinline__ float ld_dev(const float *p)
 {
     return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// two adjacent floats (8-byte aligned) in one device-scope store
+__device__ __forceinline__ void st_dev2(float *p, float a, float b)
+{
+    const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
 // two adjacent floats (8-byte aligned) in one device-scope load
 __device__ __forceinline__ float2 ld_dev2(const float *p)
 {

@@ -1216,34 +1216,31 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     }
     __syncthreads();
 
-    // ---- merge the waves into this chunk's partial
-    for (int i = tid; i < G * D; i += 64 * NW) {
-        const int h = i / D, dim = i % D;
+    // ---- merge the waves into this chunk's partial, two adjacent outputs
+    // of one head per thread (their scale factors computed once)
+    for (int i2 = tid; 2 * i2 < G * D; i2 += 64 * NW) {
+        const int h = 2 * i2 / D, dim = 2 * i2 % D;
         float M = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < NW; ww++) M = fmaxf(M, ((const float *)z_lds[ww])[h]);
-        float lt = 0.0f, ot = 0.0f;
+        float lt = 0.0f, o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
         for (int ww = 0; ww < NW; ww++) {
             const float *ml = (const float *)z_lds[ww];
             const float f = __builtin_amdgcn_exp2f(ml[h] - M);
             lt = fmaf(ml[8 + h], f, lt);
             const float *o = (const float *)(h < 4 ? v_lds0[ww] : v_lds1[ww]);
-            ot = fmaf(o[(h & 3) * D + dim], f, ot);
+            const float2 ov = *reinterpret_cast<const float2 *>(o + (h & 3) * D + dim);
+            o0 = fmaf(ov.x, f, o0);
+            o1 = fmaf(ov.y, f, o1);
         }
         float *dst = part + (((int64_t)s * n_q + kvh * qpk + h) * nb + ch) * (D + 2);
         if (ctr) {
-            st_dev(dst + 2 + dim, ot);
-            if (dim == 0) {
-                st_dev(dst, M);
-                st_dev(dst + 1, lt);
-            }
+            st_dev2(dst + 2 + dim, o0, o1);
+            if (dim == 0) st_dev2(dst, M, lt);
         } else {
-            dst[2 + dim] = ot;
-            if (dim == 0) {
-                dst[0] = M;
-                dst[1] = lt;
-            }
+            *reinterpret_cast<float2 *>(dst + 2 + dim) = make_float2(o0, o1);
+            if (dim == 0) *reinterpret_cast<float2 *>(dst) = make_float2(M, lt);
         }
     }
     if (!ctr) return;
