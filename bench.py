@@ -35,6 +35,7 @@ import ctypes as C
 import json
 import os
 import sys
+import tempfile
 import time
 from concurrent.futures import ThreadPoolExecutor
 
@@ -94,6 +95,9 @@ class Synth:
                                                 C.c_void_p]
         self.lib.eakv_synth_hold.restype = C.c_int
         self.lib.eakv_synth_hold.argtypes = [C.c_int, C.c_void_p]
+        self.lib.eakv_synth_dot_scores.restype = C.c_int
+        self.lib.eakv_synth_dot_scores.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                                   C.c_int, C.c_int, C.c_void_p]
 
     _one = None
 
@@ -126,6 +130,11 @@ class Synth:
         rc = self.lib.eakv_synth_softmax(scores, w, n_rows, L, stream)
         if rc:
             raise RuntimeError(f"softmax launch failed: {rc}")
+
+    def dot_scores(self, k, q, scores, nh, L, d, stream=None):
+        rc = self.lib.eakv_synth_dot_scores(k, q, scores, nh, L, d, stream)
+        if rc:
+            raise RuntimeError(f"dot launch failed: {rc}")
 
 
 def channel_scales(cfg, seed):
@@ -186,9 +195,10 @@ class Workload:
         c = self.cfg
         return ((s * c["nl"] + layer) * 2 + kv) * c["nkv"]
 
-    def fill_context(self):
+    def fill_context(self, log=None, every_layer=False):
         """Synthesize and quantize L0 tokens per layer of every sequence; the
-        quantize launches are timed with events."""
+        quantize launches are timed with events.  log: a progress line per
+        sequence (and per layer with every_layer), printed as each is done."""
         E, H, c = self.E, self.H, self.cfg
         slab = H.DeviceArray((2, c["nkv"], self.L0, c["d"]))
         half = c["nkv"] * self.L0 * c["d"] * 4
@@ -210,7 +220,11 @@ class Workload:
                 ev1.record(self.stream)
                 ev1.synchronize()
                 qtime += ev0.elapsed_ms(ev1)
+                if log and every_layer:
+                    log(f"bench: filled sequence {s} layer {l}")
             cache.advance(self.L0)
+            if log:
+                log(f"bench: filled sequence {s} ({c['nl']} layers x {self.L0} tokens)")
         slab.free()
         self.quant_ms = qtime
         self.quant_bytes = (c["nseq"] * c["nl"] * 2 * c["nkv"] * self.L0 * c["d"]) * (4 + 0.625)
@@ -445,11 +459,12 @@ def cpu_quantize_baseline(cfg, budget_s=4.0):
 
 # ---------------------------------------------------------------- GPU side
 
-def measure_fused(w, steps, warmup):
+def measure_fused(w, steps, warmup, log=None):
     """The decode step (append + fused attention over every layer): ms per
     step from the host clock around `steps` back-to-back steps, the fused
     calls' mean from one event pair per step on the launch stream.  A
-    growing context is rewound after the warmup steps."""
+    growing context is rewound after the warmup steps.  log: a line per
+    step once it is enqueued (runs under a profiler)."""
     H, c = w.H, w.cfg
     # a growing context has 64 spare tokens: the warmup appends at most 64
     for _ in range(min(warmup, 64) if w.grow else warmup):
@@ -462,6 +477,8 @@ def measure_fused(w, steps, warmup):
     t0 = time.perf_counter()
     for k in range(steps):
         w.step(events[k])
+        if log:
+            log(f"bench: step {k} enqueued")
     H.synchronize()
     total_s = time.perf_counter() - t0
     fused = np.array([e0.elapsed_ms(e1) / c["nl"] for e0, e1 in events]) * 1e3
@@ -585,15 +602,18 @@ def gbs(nbytes, us):
     return nbytes / (us * 1e-6) / 1e9
 
 
-def run_config(cid, steps, warmup, ctx=None, with_cpu=True, log=print):
+def run_config(cid, steps, warmup, ctx=None, with_cpu=True, log=print, grow_steps=64,
+               progress=False):
     """Fill, time and (optionally) CPU-baseline one configuration; returns
-    (summary dict, workload internals for the headline line)."""
+    (summary dict, workload internals for the headline line).  grow_steps:
+    decode steps of the growing-context workload; progress: a line per layer
+    of the fill and per timed step (for runs under a profiler)."""
     H = __import__("eakv_amd.hipmem", fromlist=["x"])
     w = Workload(cid, ctx)
     c = w.cfg
     log(f"bench: config {cid} {c['name']}: filling {c['nseq']} x {c['nl']} layers x "
         f"{w.L0} tokens")
-    w.fill_context()
+    w.fill_context(log, every_layer=progress)
     w.prepare_step_inputs()
     H.synchronize()
     qgbs = w.quant_bytes / w.quant_ms / 1e6
@@ -625,14 +645,14 @@ def run_config(cid, steps, warmup, ctx=None, with_cpu=True, log=print):
         extra = {"ms_step": u["step"] * c["nl"] / 1e3, "fused_us": u["step"], "alg": alg,
                  "steps": max(steps, 10)}
     else:
-        n_steps = 64 if c["path"] == "grow" else steps
-        ms, fused_us, fused_pct = measure_fused(w, n_steps, warmup)
+        n_steps = grow_steps if c["path"] == "grow" else steps
+        ms, fused_us, fused_pct = measure_fused(w, n_steps, warmup, log if progress else None)
         ctx_mid = w.L0 + (n_steps + 1) / 2 if c["path"] == "grow" else w.L0 + 1
         alg = int(w.fused_bytes(ctx_mid))
         r.update({
             "path": "append 1 token x all layers (batched) + eakv_attention_fused_batch_device "
-                    "x all layers" + (", context growing over 64 steps" if c["path"] == "grow"
-                                      else ", context restored each step"),
+                    "x all layers" + (f", context growing over {n_steps} steps"
+                                      if c["path"] == "grow" else ", context restored each step"),
             "steps": n_steps,
             "us_per_layer_step": round(ms * 1e3 / c["nl"], 3),
             "fused_us_per_layer": round(fused_us, 3),
@@ -656,13 +676,17 @@ def run_config(cid, steps, warmup, ctx=None, with_cpu=True, log=print):
 
 
 def reference_shapes_bench():
-    """The reference's own benchmark shapes (bench_libeakv.c:156-160: 1 layer
-    8 heads d128 at 2048 and 8192 tokens; 32 layers at 2048, measured on
-    layer 0) with its inputs (ramps (i % 2000)/200 - 5, queries 0.1) and
-    method (5 warmups, median of 20): the host-pointer eakv_attention_scores
-    and eakv_attention_output (PCIe copies and a stream wait included), the
-    device-pointer scores, and load_raw (2 warmups, median of 10); beside the
-    reference's published single-core K-score times (README.md:34-39)."""
+    """The reference's own benchmark table (bench_libeakv.c:156-240) at its
+    shapes (1 layer 8 heads d128 at 2048 and 8192 tokens; 32 layers at 2048,
+    measured on layer 0) with its inputs (ramps (i % 2000)/200 - 5, queries
+    0.1) and method (5 warmups, median of 20): the host-pointer
+    eakv_attention_scores and eakv_attention_output (PCIe copies and a stream
+    wait included), the device-pointer scores, load_raw (2 warmups, median of
+    10), its two K-score baselines on the device (dequantize the K plane to
+    f32 with eakv_dequantize_range_device, then a plain f32 dot, :76-98; the
+    f32 dot on the raw f32 K alone, :110-122) and .eakv save and load (1
+    warmup, median of 5, :222-223); beside the reference's published
+    single-core K-score times (README.md:34-39)."""
     import eakv_amd as E
     from eakv_amd import hipmem as H
     published = {(1, 2048): 210, (1, 8192): 844, (32, 2048): 213}
@@ -700,17 +724,49 @@ def reference_shapes_bench():
             assert L.eakv_attention_scores_device(c.h, dq.ptr, 0, nh, nh, ds.ptr, None) == 0
             c.sync()
         t_dev = med(dev, 5, 20)
+        # dequant + dot: layer 0's K plane (all heads: the cache's
+        # max_seq_len is sl, so the plane is [head][token][dim]) to f32, then
+        # the plain dot; and the plain dot on the raw f32 K
+        sy = Synth.get()
+        n_groups = nh * sl * hd // 64
+        kf = H.DeviceArray((nh, sl, hd))
+        raw_k = H.DeviceArray.from_host(data[: nh * sl * hd].reshape(nh, sl, hd))
+
+        def deq_dot():
+            assert L.eakv_dequantize_range_device(c.h, 0, 0, 0, n_groups, kf.ptr, None) == 0
+            sy.dot_scores(kf.ptr, dq.ptr, ds.ptr, nh, sl, hd, c.stream)
+            c.sync()
+
+        def f32_dot():
+            sy.dot_scores(raw_k.ptr, dq.ptr, ds.ptr, nh, sl, hd, c.stream)
+            c.sync()
+
+        t_deq_dot = med(deq_dot, 5, 20)
+        t_f32_dot = med(f32_dot, 5, 20)
+        path = os.path.join(tempfile.gettempdir(), f"bench_eakv_{os.getpid()}.eakv")
+        t_save = med(lambda: c.save(path), 1, 5)
+        loaded = []
+        t_load_file = med(lambda: loaded.append(E.Cache.load(path)) or loaded.pop().free(), 1, 5)
+        file_mb = os.path.getsize(path) / 1e6
+        os.unlink(path)
         res.append({"shape": f"{nl} layer(s), 8 heads, d128, {sl} tokens",
                     "published_cpu_k_score_us": published[(nl, sl)],
                     "host_api_k_score_us": round(t_ks, 1), "host_api_v_output_us": round(t_vs, 1),
                     "device_api_k_score_us_with_sync": round(t_dev, 1),
-                    "host_api_load_raw_us": round(t_load, 1)})
-        for a in (dq, ds):
+                    "device_dequant_then_dot_us_with_sync": round(t_deq_dot, 1),
+                    "device_f32_dot_us_with_sync": round(t_f32_dot, 1),
+                    "host_api_load_raw_us": round(t_load, 1),
+                    "save_eakv_us": round(t_save, 1), "load_eakv_us": round(t_load_file, 1),
+                    "eakv_file_mb": round(file_mb, 2)})
+        for a in (dq, ds, kf, raw_k):
             a.free()
         c.free()
     return {"method": "bench_libeakv.c: inputs (i % 2000)/200 - 5, queries 0.1, median of 20 "
-                      "after 5 warmups (load_raw: 10 after 2), host clock; host_api_* include "
-                      "the H2D copy of the inputs, the D2H copy of the results and the wait",
+                      "after 5 warmups (load_raw: 10 after 2; save and load of the .eakv "
+                      "file: 5 after 1), host clock; host_api_* include the H2D copy of the "
+                      "inputs, the D2H copy of the results and the wait; device_* are "
+                      "device-pointer calls followed by a wait; the load of the file "
+                      "includes creating and freeing the cache",
             "shapes": res}
 
 
@@ -728,6 +784,12 @@ def main():
     ap.add_argument("--ctx", type=int, default=None, help="override context length "
                     "(with --config)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--grow-steps", type=int, default=64, choices=range(1, 65),
+                    metavar="1..64", help="decode steps of the growing-context workload "
+                    "(its definition: 64)")
+    ap.add_argument("--progress", action="store_true",
+                    help="a line per filled layer and per timed step (runs under a "
+                         "profiler, whose counters slow every launch)")
     ap.add_argument("--unfused", action="store_true",
                     help="with --config: only time the unfused K-score and V-sum calls, "
                          "print their JSON line, then exit")
@@ -764,7 +826,7 @@ def main():
     if args.dequant or args.validate or args.unfused:
         from eakv_amd import hipmem as H
         w = Workload(args.config or HEADLINE, args.ctx)
-        w.fill_context()
+        w.fill_context(log, every_layer=args.progress)
         w.prepare_step_inputs()
         H.synchronize()
         if args.dequant:
@@ -782,7 +844,8 @@ def main():
     for cid in ids:
         r, extra = run_config(cid, args.steps if cid == head_id else max(5, args.steps // 2),
                               args.warmup, args.ctx if args.config else None,
-                              with_cpu=not args.no_cpu, log=log)
+                              with_cpu=not args.no_cpu, log=log, grow_steps=args.grow_steps,
+                              progress=args.progress)
         summaries[str(cid)] = r
         if cid == head_id:
             head = (r, extra)

@@ -72,6 +72,7 @@ SIGNATURES = {
         C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp]),
     "eakv_attention_fused_batch_device_noalloc": (
         C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "eakv_attention_fused_plan": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp]),
     "eakv_dequantize_range_device": (
         C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp, _vp]),
     "eakv_dequantize_range": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int64, C.c_int64, _vp]),
@@ -283,3 +284,17 @@ def handles(caches):
     for i, c in enumerate(caches):
         arr[i] = c.h
     return arr
+
+
+FUSED_PLAN_KEYS = ("mfma", "chunks", "merged_in_launch", "tile_tokens", "waves_per_block",
+                   "tiles_per_wave", "quads", "split")
+
+
+def fused_plan(caches, n_q, n_kv, noalloc=False):
+    """The launch eakv_attention_fused_batch_device (or, noalloc, its
+    allocation-free form) makes for these caches at their current seq_len:
+    a dict over FUSED_PLAN_KEYS (eakv_attention_fused_plan)."""
+    plan = (C.c_int32 * 8)()
+    _check(lib().eakv_attention_fused_plan(handles(caches), len(caches), n_q, n_kv,
+                                           int(bool(noalloc)), plan))
+    return dict(zip(FUSED_PLAN_KEYS, list(plan)))

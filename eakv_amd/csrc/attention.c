@@ -62,18 +62,20 @@ void eakv_attention_scores(const eakv_cache_t *cc, const float *queries,
     if (eakvi_enter(c, &prev)) return;
     const size_t qb = (size_t)n_q * c->head_dim * 4;
     const size_t sb = (size_t)n_q * c->seq_len * 4;
-    int rc = eakvi_work_begin(c, c->stream, align256(qb) + sb);
-    if (rc == EAKV_OK) {
+    void *st = c->hstream;
+    int rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, align256(qb) + sb);
+    const int began = rc == EAKV_OK;
+    if (began) {
         float *dq = (float *)c->work;
         float *ds = (float *)((char *)c->work + align256(qb));
-        int e = eakvd_memcpy_h2d_async(dq, queries, qb, c->stream);
+        int e = eakvd_memcpy_h2d_async(dq, queries, qb, st);
         if (!e) e = eakvd_k_score(&c->geom, c->dev, layer, c->seq_len, dq, n_q,
-                                  n_kv, ds, c->stream);
-        if (!e && sb) e = eakvd_memcpy_d2h_async(scores_out, ds, sb, c->stream);
-        if (!e) e = eakvd_stream_sync(c->stream);
-        if (e) eakvi_hip_fail(e, "attention_scores");
-        eakvi_work_end(c, c->stream);
+                                  n_kv, ds, st);
+        if (!e && sb) e = eakvd_memcpy_d2h_async(scores_out, ds, sb, st);
+        if (e) rc = eakvi_hip_fail(e, "attention_scores");
     }
+    eakvi_host_end(c, rc, began, "attention_scores");
     eakvi_leave(prev);
 }
 
@@ -93,11 +95,9 @@ int eakv_attention_output_device(const eakv_cache_t *cc, const float *d_w,
     rc = eakvi_enter(c, &prev);
     if (rc) return rc;
     void *st = eakvi_stream_or_default(c, stream);
-    if (st != c->stream) {
-        /* the workspace is ordered on the cache's stream */
-        int e = eakvd_stream_sync(c->stream);
-        if (e) rc = eakvi_hip_fail(e, "output");
-    }
+    /* a caller's stream: after the cache's work pending on the shared
+     * stream, its workspace uses there included (a device-side wait) */
+    rc = eakvi_order_before(c, st);
     if (rc == EAKV_OK)
         rc = eakvi_work_begin(c, st, eakvd_v_sum_work_bytes(&c->geom, c->seq_len, n_q));
     if (rc == EAKV_OK) {
@@ -126,19 +126,21 @@ void eakv_attention_output(const eakv_cache_t *cc, const float *weights,
     const size_t wb = (size_t)n_q * c->seq_len * 4;
     const size_t ob = (size_t)n_q * c->head_dim * 4;
     const size_t pb = eakvd_v_sum_work_bytes(&c->geom, c->seq_len, n_q);
-    int rc = eakvi_work_begin(c, c->stream, align256(wb) + align256(ob) + pb);
-    if (rc == EAKV_OK) {
+    void *st = c->hstream;
+    int rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, align256(wb) + align256(ob) + pb);
+    const int began = rc == EAKV_OK;
+    if (began) {
         float *dw = (float *)c->work;
         float *dout = (float *)((char *)c->work + align256(wb));
         void *part = (char *)c->work + align256(wb) + align256(ob);
-        int e = wb ? eakvd_memcpy_h2d_async(dw, weights, wb, c->stream) : 0;
+        int e = wb ? eakvd_memcpy_h2d_async(dw, weights, wb, st) : 0;
         if (!e) e = eakvd_v_sum(&c->geom, c->dev, layer, c->seq_len, dw, n_q,
-                                n_kv, dout, part, c->stream);
-        if (!e) e = eakvd_memcpy_d2h_async(output_out, dout, ob, c->stream);
-        if (!e) e = eakvd_stream_sync(c->stream);
-        if (e) eakvi_hip_fail(e, "attention_output");
-        eakvi_work_end(c, c->stream);
+                                n_kv, dout, part, st);
+        if (!e) e = eakvd_memcpy_d2h_async(output_out, dout, ob, st);
+        if (e) rc = eakvi_hip_fail(e, "attention_output");
     }
+    eakvi_host_end(c, rc, began, "attention_output");
     eakvi_leave(prev);
 }
 
@@ -187,14 +189,11 @@ int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
     int prev;
     rc = eakvi_enter(c0, &prev);
     if (rc) return rc;
-    void *st = eakvi_stream_or_default(c0, stream);
-    if (st != c0->stream) {
-        int e = eakvd_stream_sync(c0->stream);
-        if (e) rc = eakvi_hip_fail(e, "fused_batch");
-    }
-    /* the other caches' planes: after the device-pointer calls enqueued on
-     * their own streams (a device-side wait, only where there are such) */
-    for (int i = 1; rc == EAKV_OK && i < n_caches; i++)
+    void *st = eakvi_batch_stream(caches, n_caches, stream);
+    /* a caller's stream: after the work pending for each cache on the shared
+     * stream (its appends, and caches[0]'s workspace uses there), by a
+     * device-side wait where there is such */
+    for (int i = 0; rc == EAKV_OK && i < n_caches; i++)
         rc = eakvi_order_before(caches[i], st);
     eakvd_batch b;
     memset(&b, 0, sizeof(b));
@@ -229,20 +228,21 @@ int eakv_attention_fused(const eakv_cache_t *cc, const float *queries,
     b.seq_len[0] = c->seq_len;
     const size_t io = align256((size_t)n_q * c->head_dim * 4);
     const size_t pb = eakvd_fused_work_bytes(&c->geom, &b, n_q);
-    rc = eakvi_work_begin(c, c->stream, 2 * io + pb);
-    if (rc == EAKV_OK) {
+    void *st = c->hstream;
+    rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, 2 * io + pb);
+    const int began = rc == EAKV_OK;
+    if (began) {
         float *dq = (float *)c->work;
         float *dout = (float *)((char *)c->work + io);
         int e = eakvd_memcpy_h2d_async(dq, queries,
-                                       (size_t)n_q * c->head_dim * 4, c->stream);
-        if (!e) e = fused_launch(&c, 1, layer, dq, n_q, n_kv, dout, c->stream);
+                                       (size_t)n_q * c->head_dim * 4, st);
+        if (!e) e = fused_launch(&c, 1, layer, dq, n_q, n_kv, dout, st);
         if (!e) e = eakvd_memcpy_d2h_async(output_out, dout,
-                                           (size_t)n_q * c->head_dim * 4,
-                                           c->stream);
-        if (!e) e = eakvd_stream_sync(c->stream);
+                                           (size_t)n_q * c->head_dim * 4, st);
         if (e) rc = eakvi_hip_fail(e, "attention_fused");
-        eakvi_work_end(c, c->stream);
     }
+    rc = eakvi_host_end(c, rc, began, "attention_fused");
     eakvi_leave(prev);
     return rc;
 }
@@ -286,9 +286,9 @@ int eakv_attention_fused_batch_device_noalloc(eakv_cache_t *const *caches,
     int prev;
     rc = eakvi_enter(c0, &prev);
     if (rc) return rc;
-    void *st = eakvi_stream_or_default(c0, stream);
-    /* the caches' own streams: device-side waits with their events, which
-     * exist from creation on */
+    void *st = eakvi_batch_stream(caches, n_caches, stream);
+    /* the work pending for the caches on the shared stream: device-side
+     * waits with their events, which exist from creation on */
     for (int i = 0; rc == EAKV_OK && i < n_caches; i++)
         rc = eakvi_order_before(caches[i], st);
     void *scr = NULL;
@@ -303,4 +303,33 @@ int eakv_attention_fused_batch_device_noalloc(eakv_cache_t *const *caches,
     }
     eakvi_leave(prev);
     return rc;
+}
+
+int eakv_attention_fused_plan(eakv_cache_t *const *caches, int n_caches, int n_q,
+                              int n_kv, int noalloc, int32_t *plan)
+{
+    if (!caches || n_caches <= 0 || n_caches > EAKVD_MAX_BATCH || !plan)
+        return eakvi_set_error(EAKV_ERR_INVALID, "fused_plan: invalid argument");
+    for (int i = 0; i < n_caches; i++)
+        if (!caches[i])
+            return eakvi_set_error(EAKV_ERR_INVALID, "fused_plan: NULL cache");
+    eakv_cache_t *c0 = caches[0];
+    int rc = attn_check(c0, 0, n_q, n_kv);
+    if (rc) return rc;
+    eakvd_batch b;
+    memset(&b, 0, sizeof(b));
+    b.n_seq = n_caches;
+    for (int i = 0; i < n_caches; i++) {
+        b.base[i] = caches[i]->dev;
+        b.seq_len[i] = caches[i]->seq_len;
+    }
+    int prev;
+    rc = eakvi_enter(c0, &prev);
+    if (rc) return rc;
+    /* the workspace form merges with caches[0]'s counters; the
+     * allocation-free form has none */
+    eakvd_fused_plan(&c0->geom, &b, n_q, n_kv, noalloc ? NULL : c0->dev + c0->geom.ctr_off,
+                     plan);
+    eakvi_leave(prev);
+    return EAKV_OK;
 }

@@ -81,10 +81,14 @@ void eakvi_leave(int prev)
 }
 
 /* Every use of the workspace is ordered after the previous one: uses on the
- * cache's own stream by that stream; a use on a caller's stream records
- * work_event there, and the next use (on any stream) waits for it.  Calls
- * that name the cache with a caller's stream host-wait for the cache's own
- * stream first (attention.c), which orders the other direction. */
+ * shared stream by that stream; a use on a caller's stream records
+ * work_event there, and the next use (on any stream) waits for it; the
+ * host-pointer calls' uses on the cache's own stream are complete when the
+ * call returns (eakvi_host_end).  A call on another stream than the shared
+ * one first waits, on the device, for the cache's work pending there
+ * (eakvi_order_before), which orders the other direction.  Growing the
+ * workspace waits on the host for every earlier use (the shared stream
+ * included) before the old buffer is freed. */
 int eakvi_work_begin(eakv_cache_t *c, void *st, size_t n)
 {
     if (c->work_on_caller) {
@@ -133,6 +137,29 @@ void *eakvi_stream_or_default(const eakv_cache_t *c, void *s)
     return c->stream;
 }
 
+void *eakvi_batch_stream(eakv_cache_t *const *caches, int n, void *s)
+{
+    if (s) return s;
+    for (int i = 0; i < n; i++) caches[i]->own_async++;
+    return caches[0]->stream;
+}
+
+int eakvi_host_begin(eakv_cache_t *c)
+{
+    return eakvi_order_before(c, c->hstream);
+}
+
+int eakvi_host_end(eakv_cache_t *c, int rc, int used_work, const char *what)
+{
+    int e = eakvd_stream_sync(c->hstream);
+    if (e && rc == EAKV_OK) rc = eakvi_hip_fail(e, what);
+    if (used_work) {
+        if (!e) c->work_on_caller = 0;      /* the use is complete */
+        else eakvi_work_end(c, c->hstream);
+    }
+    return rc;
+}
+
 /* Record c's order event on `from`; every stream in to[0..n) (other than
  * `from`) waits for it on the device.  If the event cannot be used, a host
  * wait for `from` orders the same work. */
@@ -172,7 +199,12 @@ int eakvi_order_after(eakv_cache_t *const *caches, int n, void *st)
         for (int j = 0; j < k && !seen; j++) seen = to[j] == s;
         if (!seen) to[k++] = s;
     }
-    return k ? order_wait(caches[0], st, to, k) : EAKV_OK;
+    if (!k) return EAKV_OK;
+    int rc = order_wait(caches[0], st, to, k);
+    /* the shared stream now holds a wait for st on behalf of every named
+     * cache: a later host-pointer call on one of them orders after it */
+    for (int i = 0; rc == EAKV_OK && i < n; i++) caches[i]->own_async++;
+    return rc;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -208,6 +240,9 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
     /* the device's caches share one stream (eakvd_device_stream) */
     e = eakvd_device_stream(c->device, &c->stream);
     if (e) goto hip_fail;
+    /* the host-pointer calls' own stream */
+    e = eakvd_stream_create(&c->hstream);
+    if (e) goto hip_fail;
     /* created here so that ordering a batched call allocates nothing */
     e = eakvd_event_create(&c->order_event);
     if (e) goto hip_fail;
@@ -215,8 +250,8 @@ eakv_cache_t *eakv_cache_create(int n_layers, int n_kv_heads, int head_dim,
     if (e) goto hip_fail;
     /* the reference calloc()s its planes (cache.c:33); the counters start
      * at zero */
-    e = eakvd_memset_async(c->dev, 0, c->dev_bytes, c->stream);
-    if (!e) e = eakvd_stream_sync(c->stream);
+    e = eakvd_memset_async(c->dev, 0, c->dev_bytes, c->hstream);
+    if (!e) e = eakvd_stream_sync(c->hstream);
     if (e) goto hip_fail;
     return c;
 
@@ -224,6 +259,7 @@ hip_fail:
     eakvi_hip_fail(e, "cache_create");
     if (c->dev) eakvd_free(c->dev);
     if (c->order_event) eakvd_event_destroy(c->order_event);
+    if (c->hstream) eakvd_stream_destroy(c->hstream);
     free(c);
     return NULL;
 }
@@ -234,9 +270,11 @@ void eakv_cache_free(eakv_cache_t *c)
     int prev;
     int ok = eakvi_enter(c, &prev) == EAKV_OK;
     if (c->stream) eakvd_stream_sync(c->stream);
+    if (c->hstream) eakvd_stream_sync(c->hstream);
     if (c->work_on_caller) eakvd_event_sync(c->work_event);
     if (c->work_event) eakvd_event_destroy(c->work_event);
     if (c->order_event) eakvd_event_destroy(c->order_event);
+    if (c->hstream) eakvd_stream_destroy(c->hstream);
     if (c->work) eakvd_free(c->work);
     if (c->dev) eakvd_free(c->dev);
     if (ok) eakvi_leave(prev);
@@ -287,22 +325,20 @@ int eakv_cache_load_raw(eakv_cache_t *c, const float *data, int seq_len)
     int per = (int)((256ll << 20) / (plane_bytes ? plane_bytes : 1));
     if (per < 1) per = 1;
     if (per > n_planes) per = n_planes;
-    rc = eakvi_work_begin(c, c->stream, (size_t)plane_bytes * per);
+    void *st = c->hstream;
+    rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, (size_t)plane_bytes * per);
     const int began = rc == EAKV_OK;
     for (int p0 = 0; rc == EAKV_OK && p0 < n_planes; p0 += per) {
         int np = n_planes - p0 < per ? n_planes - p0 : per;
         int e = eakvd_memcpy_h2d_async(c->work, data + (int64_t)p0 * row_elems *
                                                             c->n_kv_heads,
-                                       (size_t)plane_bytes * np, c->stream);
+                                       (size_t)plane_bytes * np, st);
         if (e) { rc = eakvi_hip_fail(e, "load_raw H2D"); break; }
         rc = quant_rows(c, (const float *)c->work, row_elems, p0, np, seq_len,
-                        0, c->stream);
+                        0, st);
     }
-    if (rc == EAKV_OK) {
-        int e = eakvd_stream_sync(c->stream);
-        if (e) rc = eakvi_hip_fail(e, "load_raw");
-    }
-    if (began) eakvi_work_end(c, c->stream);
+    rc = eakvi_host_end(c, rc, began, "load_raw");
     if (rc == EAKV_OK) c->seq_len = seq_len;
     eakvi_leave(prev);
     return rc;
@@ -350,20 +386,18 @@ int eakv_cache_append(eakv_cache_t *c, const float *data, int layer,
     if (rc) return rc;
     const int64_t row_elems = (int64_t)n_tokens * c->head_dim;
     const size_t bytes = (size_t)row_elems * c->n_kv_heads * 4;
-    rc = eakvi_work_begin(c, c->stream, bytes);
+    void *st = c->hstream;
+    rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, bytes);
     const int began = rc == EAKV_OK;
     if (rc == EAKV_OK) {
-        int e = eakvd_memcpy_h2d_async(c->work, data, bytes, c->stream);
+        int e = eakvd_memcpy_h2d_async(c->work, data, bytes, st);
         if (e) rc = eakvi_hip_fail(e, "append H2D");
     }
     if (rc == EAKV_OK)
         rc = quant_rows(c, (const float *)c->work, row_elems,
-                        layer * 2 + kv_idx, 1, n_tokens, c->seq_len, c->stream);
-    if (rc == EAKV_OK) {
-        int e = eakvd_stream_sync(c->stream);
-        if (e) rc = eakvi_hip_fail(e, "append");
-    }
-    if (began) eakvi_work_end(c, c->stream);
+                        layer * 2 + kv_idx, 1, n_tokens, c->seq_len, st);
+    rc = eakvi_host_end(c, rc, began, "append");
     eakvi_leave(prev);
     return rc;
 }
@@ -407,7 +441,7 @@ int eakv_append_batch_device(eakv_cache_t *const *caches, int n_caches,
     eakv_cache_t *c0 = caches[0];
     int prev, rc = eakvi_enter(c0, &prev);
     if (rc) return rc;
-    void *st = eakvi_stream_or_default(c0, stream);
+    void *st = eakvi_batch_stream(caches, n_caches, stream);
     /* the launch writes every cache: after their streams' earlier work */
     for (int i = 0; rc == EAKV_OK && i < n_caches; i++)
         rc = eakvi_order_before(caches[i], st);
@@ -502,17 +536,20 @@ int eakv_cache_read_planes(const eakv_cache_t *c, int layer, int kv_idx,
         return eakvi_set_error(EAKV_ERR_INVALID, "read_planes: invalid argument");
     int prev, rc = eakvi_enter(c, &prev);
     if (rc) return rc;
+    eakv_cache_t *cm = (eakv_cache_t *)c;
     const uint8_t *blk =
         c->dev + (int64_t)(layer * 2 + kv_idx) * c->geom.block_bytes;
     const size_t ng = (size_t)c->geom.max_groups;
+    void *st = c->hstream;
+    rc = eakvi_host_begin(cm);
     int e = 0;
-    if (weights) e = eakvd_memcpy_d2h_async(weights, blk, ng * 32, c->stream);
-    if (!e && scales)
-        e = eakvd_memcpy_d2h_async(scales, blk + c->geom.s_off, ng * 4, c->stream);
-    if (!e && biases)
-        e = eakvd_memcpy_d2h_async(biases, blk + c->geom.b_off, ng * 4, c->stream);
-    if (!e) e = eakvd_stream_sync(c->stream);
+    if (rc == EAKV_OK && weights) e = eakvd_memcpy_d2h_async(weights, blk, ng * 32, st);
+    if (rc == EAKV_OK && !e && scales)
+        e = eakvd_memcpy_d2h_async(scales, blk + c->geom.s_off, ng * 4, st);
+    if (rc == EAKV_OK && !e && biases)
+        e = eakvd_memcpy_d2h_async(biases, blk + c->geom.b_off, ng * 4, st);
     if (e) rc = eakvi_hip_fail(e, "read_planes");
+    rc = eakvi_host_end(cm, rc, 0, "read_planes");
     eakvi_leave(prev);
     return rc;
 }

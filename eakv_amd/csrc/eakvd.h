@@ -62,6 +62,8 @@ int  eakvd_free(void *p);
 int  eakvd_host_malloc(void **p, size_t n);   /* pinned */
 int  eakvd_host_free(void *p);
 int  eakvd_device_stream(int dev, void **s);   /* the caches' stream of device dev */
+int  eakvd_stream_create(void **s);           /* non-blocking, default priority */
+int  eakvd_stream_destroy(void *s);
 int  eakvd_stream_sync(void *s);
 int  eakvd_event_create(void **e);            /* no timing */
 int  eakvd_event_destroy(void *e);
@@ -137,6 +139,14 @@ size_t eakvd_fused_work_bytes(const eakvd_geom *g, const eakvd_batch *b,
 int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b, int layer,
                 const float *q, int n_q, int n_kv, float *out, void *work,
                 void *ctr, void *stream);
+/* The launch eakvd_fused makes for this batch, head split and counter
+ * region (ctr as eakvd_fused's): out[0] 1 for the matrix-core program (0:
+ * the VALU program), [1] chunks per (sequence, virtual kv head) unit, [2] 1
+ * when the chunks merge inside the launch (0: a merge launch follows), [3]
+ * tokens per tile, [4] waves per block, [5] the most tiles a wave walks,
+ * [6] quads of q heads per wave, [7] virtual kv heads per kv head. */
+void eakvd_fused_plan(const eakvd_geom *g, const eakvd_batch *b, int n_q, int n_kv,
+                      const void *ctr, int32_t *out);
 /* The bytes of partials that eakvd_fused writes and reads for this batch
  * and head split (at most eakvd_fused_work_bytes()). */
 size_t eakvd_fused_launch_bytes(const eakvd_geom *g, const eakvd_batch *b,

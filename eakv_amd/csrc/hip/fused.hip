@@ -68,10 +68,7 @@ constexpr int kWaves = 4;
 // read the planes faster than 4 blocks (16 waves), and a unit has half the
 // chunks to merge (8 x 32Q/8KV at 32767 tokens, merged in the launch: 63.1-64.5
 // against 64.3-67.5 us per call with 4 blocks and a merge launch)
-#ifndef EAKV_FUSED_BLOCKS_PER_CU
-#define EAKV_FUSED_BLOCKS_PER_CU 2
-#endif
-constexpr int kBlocksPerCU = EAKV_FUSED_BLOCKS_PER_CU;   // occupancy the register budget is set for
+constexpr int kBlocksPerCU = 2;   // occupancy the register budget is set for
 // Blocks of the kernel for HH quads of q heads per wave.  One quad: blocks
 // of kWaves waves, kBlocksPerCU resident per CU.  Two quads: blocks of 8
 // waves (d = 128: one per CU, 2 waves per SIMD, as the registers allow;
@@ -88,17 +85,7 @@ constexpr float kTau = 8.0f;            // lazy-rescale headroom, 2^8 (log2 unit
 // heads, d = 128, 131071 tokens: 39.2 against 40.0-40.6 us per call;
 // 8 x 32Q/8KV at 32767 tokens: 65.7-66.0 against 66.1-68.6 (per-step
 // medians); 32Q/32KV at 8192 tokens: 14.0-14.3 against 15.0.
-#ifndef EAKV_FUSED_SLOTS
-#define EAKV_FUSED_SLOTS 2
-#endif
-constexpr int kSlots = EAKV_FUSED_SLOTS;
-#ifndef EAKV_SHARE_Q
-#define EAKV_SHARE_Q 1
-#endif
-constexpr bool kShareQ = EAKV_SHARE_Q;
-#ifndef EAKV_OOB_TAIL
-#define EAKV_OOB_TAIL 1
-#endif    // one wave per quad computes the q operands
+constexpr int kSlots = 2;
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void *lds_ptr;
@@ -602,15 +589,11 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // and does not make reads of a slot wait for younger loads to LDS.
     static_assert(Geo<D, TT>::VSLOT >= 4 * D * 4, "outputs fit a V slot");
     static_assert(HH == 1 || HH == 2, "one or two quads");
-    static_assert(kSlots <= 4, "slot variables");
+    static_assert(kSlots == 2, "two slot variables");
     __shared__ __attribute__((aligned(16))) uint8_t v_lds0[NW][Geo<D, TT>::VSLOT];
     __shared__ __attribute__((aligned(16))) uint8_t v_lds1[NW][Geo<D, TT>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds2[kSlots > 2 ? NW : 1][Geo<D, TT>::VSLOT];
-    __shared__ __attribute__((aligned(16))) uint8_t v_lds3[kSlots > 3 ? NW : 1][Geo<D, TT>::VSLOT];
     __shared__ __attribute__((aligned(16))) float s_lds0[NW][Geo<D, TT>::SSLOT];
     __shared__ __attribute__((aligned(16))) float s_lds1[NW][Geo<D, TT>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds2[kSlots > 2 ? NW : 1][Geo<D, TT>::SSLOT];
-    __shared__ __attribute__((aligned(16))) float s_lds3[kSlots > 3 ? NW : 1][Geo<D, TT>::SSLOT];
     __shared__ __attribute__((aligned(16))) uint8_t z_lds[NW][HH * Geo<D, TT>::ZROWS * 8];
 
     const int ch = blockIdx.x, nb = gridDim.x, kvh = blockIdx.y, s = blockIdx.z;
@@ -656,7 +639,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
 #pragma unroll
     for (int hq = 0; hq < HH; hq++) {
         qrow[hq] = 4 * hq + ha < G;
-        if (kShareQ && w != hq) continue;
+        if (w != hq) continue;
         const float4 *qh4 = (const float4 *)(qs + (qrow[hq] ? 4 * hq + ha : 0) * D);
 #pragma unroll
         for (int gg = 0; gg < GPD; gg++)
@@ -739,16 +722,12 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     auto vslot = [&](auto kc) -> uint8_t * {
         constexpr int k = decltype(kc)::value;
         if constexpr (k == 0) return v_lds0[w];
-        else if constexpr (k == 1) return v_lds1[w];
-        else if constexpr (k == 2) return v_lds2[w];
-        else return v_lds3[w];
+        else return v_lds1[w];
     };
     auto sslot = [&](auto kc) -> float * {
         constexpr int k = decltype(kc)::value;
         if constexpr (k == 0) return s_lds0[w];
-        else if constexpr (k == 1) return s_lds1[w];
-        else if constexpr (k == 2) return s_lds2[w];
-        else return s_lds3[w];
+        else return s_lds1[w];
     };
     using I0 = std::integral_constant<int, 0>;
 
@@ -764,7 +743,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // every plane: the loads return 0 at once, with no memory request), so
     // a wave's last groups, never consumed except as masked tokens, do not
     // hold up its epilogue.  The tile offset stays clamped in range.
-    auto oob = [&](int t) -> uint32_t { return EAKV_OOB_TAIL && t >= n_tiles ? 0x80000000u : 0u; };
+    auto oob = [&](int t) -> uint32_t { return t >= n_tiles ? 0x80000000u : 0u; };
 
     StageT st[kSlots];
     // group j: V of tile T(j-1) into V slot (j-1) % kSlots, then the scales
@@ -798,8 +777,6 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     else load_k<D, TT>(st[0], P, ldt(tk[0]), oob(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
     load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
-    if constexpr (kSlots > 2) load_group(std::integral_constant<int, 2>{}, tk[1], tk[2]);
-    if constexpr (kSlots > 3) load_group(std::integral_constant<int, 3>{}, tk[2], tk[3]);
 
     // scores are kept in the log2 domain (times log2(e))
     const float rs2 = rs * EAKV_LOG2E;
@@ -808,7 +785,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     if constexpr (!VS)
 #pragma unroll
     for (int hq = 0; hq < HH; hq++) {
-    if (kShareQ && w != hq) continue;
+    if (w != hq) continue;
     float amax = 0.0f;
     float qsum[GPD];
 #pragma unroll
@@ -854,7 +831,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
 #pragma unroll
     for (int gg = 0; gg < GPD; gg++) bq[hq][gg] = rs2 * __shfl(qsum[gg], 4 * ho, 64);
     }
-    if constexpr (!VS && kShareQ) {
+    if constexpr (!VS) {
         // quad hq's operands of lane l: dwords (hq*QR + f)*64 + l of the
         // digit rows, which no wave uses before its first tile's weights
         constexpr int QR = GPD * 4 + 2 + GPD;
@@ -1178,10 +1155,6 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         for (;;) {
             if (!iter(std::integral_constant<int, 0>{})) { keep(); break; }
             if (!iter(std::integral_constant<int, 1>{})) { keep(); break; }
-            if constexpr (kSlots > 2)
-                if (!iter(std::integral_constant<int, 2>{})) { keep(); break; }
-            if constexpr (kSlots > 3)
-                if (!iter(std::integral_constant<int, 3>{})) { keep(); break; }
         }
     }
     // loads into LDS still in flight (the clamped groups past the end) must
@@ -1448,10 +1421,7 @@ constexpr int kChunkV = 512;      // tokens per block
 // the MFMA program's chunks hold at least kChunkM tokens (the partials'
 // workspace is sized by it): 8 tiles, 2 per wave of a 4-wave block
 // (mfma_blocks_per_unit)
-#ifndef EAKV_CHUNK_M
-#define EAKV_CHUNK_M 256
-#endif
-constexpr int kChunkM = EAKV_CHUNK_M;
+constexpr int kChunkM = 256;
 constexpr int kHeadsLds = 16;     // q heads per pass
 
 template <int D>
@@ -1768,10 +1738,34 @@ extern "C" int eakvd_scratch(void **p)
 // chunks per unit) it cost more.
 bool merge_in_launch(const eakvd_geom *g, const void *ctr, int mc, int64_t units)
 {
-#ifdef EAKV_NO_MERGE_IN_LAUNCH
-    return false;
-#endif
     return ctr && mc <= kInBatch && units <= g->ctr_slots;
+}
+
+extern "C" void eakvd_fused_plan(const eakvd_geom *g, const eakvd_batch *b, int n_q, int n_kv,
+                                 const void *ctr, int32_t *out)
+{
+    const FusedPlan p = fused_plan(g, b, n_q, n_kv);
+    const int ml = max_len(b);
+    out[0] = p.mfma;
+    out[1] = p.mc;
+    if (p.mfma) {
+        const int64_t units = (int64_t)n_kv * p.split * b->n_seq;
+        const int64_t n_tiles = ((int64_t)ml + p.tt - 1) / p.tt;
+        const int64_t waves = (int64_t)p.mc * p.wpb;
+        out[2] = merge_in_launch(g, ctr, p.mc, units);
+        out[3] = p.tt;
+        out[4] = p.wpb;
+        out[5] = (int32_t)((n_tiles + waves - 1) / waves);
+        out[6] = p.hh;
+        out[7] = p.split;
+    } else {
+        out[2] = 0;
+        out[3] = kChunkV;
+        out[4] = 4;
+        out[5] = 1;
+        out[6] = 0;
+        out[7] = 1;
+    }
 }
 
 extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,

@@ -21,14 +21,8 @@
 
 namespace {
 
-#ifndef EAKV_KS_BUFS
-#define EAKV_KS_BUFS 2
-#endif
-#ifndef EAKV_KS_BLOCKS_PER_CU
-#define EAKV_KS_BLOCKS_PER_CU 2
-#endif
-constexpr int kKsBufs = EAKV_KS_BUFS;               // slices per wave in flight, one consumed
-constexpr int kKsBlocksPerCU = EAKV_KS_BLOCKS_PER_CU;
+constexpr int kKsBufs = 2;                          // slices per wave in flight, one consumed
+constexpr int kKsBlocksPerCU = 2;
 
 template <int J>
 __device__ __forceinline__ void dequant4(float *klo, float *khi, uint32_t lo, uint32_t hi,
@@ -202,12 +196,9 @@ __global__ __launch_bounds__(256) void k_score_kernel(
     k_score_body<D, false>(kw, ks, kb, gph, L, q, qpk, scores, rs);
 }
 
-#ifndef EAKV_KS_MHA_WAVES
-#define EAKV_KS_MHA_WAVES 2
-#endif
-// One q head per kv head: registers for EAKV_KS_MHA_WAVES waves per SIMD.
+// One q head per kv head: registers for 2 waves per SIMD.
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EAKV_KS_MHA_WAVES)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_score_mha_kernel(
     const uint8_t *__restrict__ kw, const float *__restrict__ ks,
     const float *__restrict__ kb, int64_t gph, int L,

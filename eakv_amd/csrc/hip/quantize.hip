@@ -21,10 +21,7 @@
 
 namespace {
 
-#ifndef EAKV_QUANT_BLOCKS
-#define EAKV_QUANT_BLOCKS 8192
-#endif
-constexpr int64_t kQuantBlocks = EAKV_QUANT_BLOCKS;
+constexpr int64_t kQuantBlocks = 8192;
 constexpr int64_t kOnePass = 32768;
 
 // One group: the reference's min/max, scale, bias and nibbles; lane j's

@@ -52,6 +52,17 @@ int eakvd_device_stream(int dev, void **s)
     return 0;
 }
 
+// A stream of one cache's own (its synchronous host-pointer calls)
+int eakvd_stream_create(void **s)
+{
+    hipStream_t st = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+    *s = (void *)st;
+    return (int)e;
+}
+
+int eakvd_stream_destroy(void *s) { return s ? (int)hipStreamDestroy((hipStream_t)s) : 0; }
+
 int eakvd_stream_sync(void *s) { return (int)hipStreamSynchronize((hipStream_t)s); }
 
 int eakvd_event_create(void **e)

@@ -45,17 +45,20 @@ int eakv_dequantize_range(const eakv_cache_t *cc, int layer, int kv_idx,
     /* staged through the workspace, at most 64 MiB of f32 per pass */
     const int64_t per = (int64_t)1 << 18;              /* groups: 64 MiB */
     const int64_t chunk = group_count < per ? group_count : per;
-    rc = eakvi_work_begin(c, c->stream, (size_t)chunk * 256);
+    void *st = c->hstream;
+    rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, (size_t)chunk * 256);
     const int began = rc == EAKV_OK;
-    for (int64_t g = 0; rc == EAKV_OK && g < group_count; g += chunk) {
+    for (int64_t g = 0; began && rc == EAKV_OK && g < group_count; g += chunk) {
         const int64_t n = group_count - g < chunk ? group_count - g : chunk;
         int e = eakvd_dequantize(&c->geom, c->dev, layer, kv_idx, group_start + g, n,
-                                 (float *)c->work, c->stream);
-        if (!e) e = eakvd_memcpy_d2h_async(out + g * 64, c->work, (size_t)n * 256, c->stream);
-        if (!e) e = eakvd_stream_sync(c->stream);
+                                 (float *)c->work, st);
+        if (!e) e = eakvd_memcpy_d2h_async(out + g * 64, c->work, (size_t)n * 256, st);
         if (e) rc = eakvi_hip_fail(e, "dequantize_range");
+        /* the next pass reuses the workspace: wait for this one */
+        else if (g + chunk < group_count) rc = eakvi_host_end(c, rc, 0, "dequantize_range");
     }
-    if (began) eakvi_work_end(c, c->stream);
+    rc = eakvi_host_end(c, rc, began, "dequantize_range");
     eakvi_leave(prev);
     return rc;
 }
@@ -75,15 +78,16 @@ int eakv_validate(const eakv_cache_t *cc, int32_t *results)
         eakvi_leave(prev);
         return eakvi_set_error(EAKV_ERR_ALLOC, "validate: out of host memory");
     }
-    rc = eakvi_work_begin(c, c->stream, (size_t)nb * sizeof(*h));
-    if (rc == EAKV_OK) {
-        int e = eakvd_validate(&c->geom, c->dev, nb, n, (unsigned long long *)c->work,
-                               c->stream);
-        if (!e) e = eakvd_memcpy_d2h_async(h, c->work, (size_t)nb * sizeof(*h), c->stream);
-        if (!e) e = eakvd_stream_sync(c->stream);
+    void *st = c->hstream;
+    rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, (size_t)nb * sizeof(*h));
+    const int began = rc == EAKV_OK;
+    if (began) {
+        int e = eakvd_validate(&c->geom, c->dev, nb, n, (unsigned long long *)c->work, st);
+        if (!e) e = eakvd_memcpy_d2h_async(h, c->work, (size_t)nb * sizeof(*h), st);
         if (e) rc = eakvi_hip_fail(e, "validate");
-        eakvi_work_end(c, c->stream);
     }
+    rc = eakvi_host_end(c, rc, began, "validate");
     if (rc == EAKV_OK)
         for (int i = 0; i < nb; i++) results[i] = h[i] == ~0ull ? 0 : (int32_t)(h[i] & 3);
     free(h);

@@ -23,7 +23,11 @@ struct eakv_cache {
     uint8_t   *dev;        /* planes */
     size_t     dev_bytes;
     void      *stream;     /* the device's caches' stream (eakvd_device_stream):
-                              default priority, non-blocking, shared */
+                              default priority, non-blocking, shared; the
+                              device-pointer calls' default */
+    void      *hstream;    /* this cache's own stream (default priority,
+                              non-blocking): the synchronous host-pointer
+                              calls of the reference API run and wait here */
 
     void  *work;           /* device scratch for staging and partials */
     size_t work_bytes;
@@ -63,7 +67,21 @@ int  eakvi_order_before(eakv_cache_t *c, void *st);
 int  eakvi_order_after(eakv_cache_t *const *caches, int n, void *st);
 
 /* The stream a device-pointer call runs on: the caller's, or (NULL) the
- * cache's own, which the call then counts as pending work on it. */
+ * device's shared stream, which the call then counts as pending work of the
+ * cache on it. */
 void *eakvi_stream_or_default(const eakv_cache_t *c, void *s);
+/* The same for a call that names the caches [0, n): with a NULL stream the
+ * launch is counted as pending work of every one of them. */
+void *eakvi_batch_stream(eakv_cache_t *const *caches, int n, void *s);
+
+/* Synchronous host-pointer calls (the reference API) run on c->hstream.
+ * eakvi_host_begin orders hstream after the cache's device-pointer work still
+ * pending on the shared stream (a device-side wait, only when there is
+ * such); eakvi_host_end waits for hstream alone and, when that succeeds,
+ * marks the workspace use st == hstream complete (otherwise it stays ordered
+ * by its event).  Two threads working on distinct caches therefore wait for
+ * their own work only.  Returns rc, or the wait's error if rc is EAKV_OK. */
+int  eakvi_host_begin(eakv_cache_t *c);
+int  eakvi_host_end(eakv_cache_t *c, int rc, int used_work, const char *what);
 
 #endif

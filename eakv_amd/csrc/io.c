@@ -145,13 +145,13 @@ int eakv_cache_load(const char *path, eakv_cache_t **out)
             break;
         }
         uint8_t *blk = c->dev + (int64_t)i * c->geom.block_bytes;
-        int e = eakvd_memcpy_h2d_async(blk, stage, (size_t)n_groups * 32, c->stream);
+        int e = eakvd_memcpy_h2d_async(blk, stage, (size_t)n_groups * 32, c->hstream);
         if (!e) e = eakvd_memcpy_h2d_async(blk + c->geom.s_off, stage + n_groups * 32,
-                                           (size_t)n_groups * 4, c->stream);
+                                           (size_t)n_groups * 4, c->hstream);
         if (!e) e = eakvd_memcpy_h2d_async(blk + c->geom.b_off, stage + n_groups * 36,
-                                           (size_t)n_groups * 4, c->stream);
-        if (!e) e = eakvd_stream_sync(c->stream);
+                                           (size_t)n_groups * 4, c->hstream);
         if (e) rc = eakvi_hip_fail(e, "load H2D");
+        rc = eakvi_host_end(c, rc, 0, "load H2D");
     }
     if (entered) eakvi_leave(prev);
     free(offs);

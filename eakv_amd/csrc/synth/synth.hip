@@ -202,6 +202,47 @@ extern "C" int eakv_synth_softmax(const float *scores, float *w, int n_rows, int
     return (int)hipGetLastError();
 }
 
+namespace {
+
+// scores[h][t] = (q[h] . k[h][t]) / sqrt(d) on f32 rows k[(h*L + t)*d ..],
+// one thread per (h, t), the dims in order (a plain dot, no quantization).
+__global__ __launch_bounds__(256) void dot_kernel(const float *__restrict__ k,
+                                                  const float *__restrict__ q,
+                                                  float *__restrict__ scores, int nh, int L,
+                                                  int d, float rs)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)nh * L) return;
+    const int h = (int)(i / L);
+    const float4 *kr = reinterpret_cast<const float4 *>(k + i * d);
+    const float4 *qr = reinterpret_cast<const float4 *>(q + (int64_t)h * d);
+    float sum = 0.0f;
+    for (int c = 0; c < d / 4; c++) {
+        const float4 a = kr[c], b = qr[c];
+        sum = fmaf(a.x, b.x, sum);
+        sum = fmaf(a.y, b.y, sum);
+        sum = fmaf(a.z, b.z, sum);
+        sum = fmaf(a.w, b.w, sum);
+    }
+    scores[i] = sum * rs;
+}
+
+}  // namespace
+
+// The reference benchmark's dot baselines (benchmarks/bench_libeakv.c:76-122)
+// on the device: scores[nh][L] = q[nh][d] . k[nh][L][d] / sqrt(d), d a
+// multiple of 4, all pointers 16-byte aligned.
+extern "C" int eakv_synth_dot_scores(const float *k, const float *q, float *scores, int nh,
+                                     int L, int d, void *stream)
+{
+    if (nh <= 0 || L <= 0) return 0;
+    if ((d & 3) || ((uintptr_t)k & 15) || ((uintptr_t)q & 15)) return (int)hipErrorInvalidValue;
+    const int64_t n = (int64_t)nh * L;
+    hipLaunchKernelGGL(dot_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, k, q, scores, nh, L, d, 1.0f / sqrtf((float)d));
+    return (int)hipGetLastError();
+}
+
 // Compute units of the current device (0 if the query fails).
 extern "C" int eakv_synth_cu_count(void)
 {

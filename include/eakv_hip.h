@@ -4,10 +4,10 @@
  * memory.  They exist because the reference API takes host pointers, which
  * forces a PCIe round trip per call on a GPU:
  *   - device-pointer forms of load/append/scores/output, asynchronous on a
- *     HIP stream (pass the hipStream_t as void*, NULL = the cache's own:
- *     one non-blocking stream per device, shared by every cache created on
- *     that device, so the device's caches' default-stream work runs in
- *     enqueue order);
+ *     HIP stream (pass the hipStream_t as void*; NULL = the device's shared
+ *     stream: one non-blocking stream per device, shared by every cache
+ *     created on that device, so the device's caches' default-stream work
+ *     runs in enqueue order);
  *   - batched append and batched fused decode attention over several caches
  *     of the same shape (one launch per layer for all sequences);
  *   - the fused single-pass softmax attention, which the reference compiles
@@ -16,12 +16,18 @@
  *   - dequantization and the integrity check of GPU-resident planes, which the
  *     reference runs on its host planes from its benchmark and CLI.
  * Device-pointer calls return when the work is enqueued; results are ready
- * after eakv_cache_sync() or a wait on the stream.  Calls on one cache that
- * use its device workspace (V-sum and fused partials, host staging) are
- * ordered among themselves whatever their streams (an event recorded on a
- * caller's stream, waited for by the next use); any other ordering between
- * streams (e.g. K/V appended on one caller's stream and read on another) is
- * the caller's, as for any work on two streams.
+ * after eakv_cache_sync() or a wait on the stream.  The host-pointer calls
+ * of include/eakv.h (and eakv_attention_fused, eakv_cache_read_planes,
+ * eakv_dequantize_range, eakv_validate, eakv_cache_save/load) run on a
+ * stream of the cache's own, after the device-pointer work still pending for
+ * that cache on the shared stream, and wait for that stream alone: calls on
+ * distinct caches from distinct threads do not wait for one another (the
+ * reference's "thread-safe for distinct caches", include/eakv.h:3).  Calls
+ * on one cache that use its device workspace (V-sum and fused partials, host
+ * staging) are ordered among themselves whatever their streams (an event
+ * recorded on a caller's stream, waited for by the next use); any other
+ * ordering between caller streams (e.g. K/V appended on one caller's stream
+ * and read on another) is the caller's, as for any work on two streams.
  */
 #ifndef EAKV_HIP_H
 #define EAKV_HIP_H
@@ -44,9 +50,9 @@ int         eakv_last_error(void);
 const char *eakv_last_error_message(void);
 void        eakv_clear_error(void);
 
-/* The HIP device ordinal the cache lives on, its stream (the device's
- * caches' shared stream), and a wait for all work enqueued on that stream
- * (by any cache of the device). */
+/* The HIP device ordinal the cache lives on, the device's shared stream (the
+ * NULL-stream default of the device-pointer calls), and a wait for all work
+ * enqueued on that stream (by any cache of the device). */
 int   eakv_cache_device(const eakv_cache_t *cache);
 void *eakv_cache_stream(const eakv_cache_t *cache);
 int   eakv_cache_sync(const eakv_cache_t *cache);
@@ -68,9 +74,9 @@ int eakv_cache_append_device(eakv_cache_t *cache, const float *d_data,
  * launch.  d_data: f32[n_caches][n_layers][2][n_kv_heads][n_tokens][head_dim].
  * Caches must share n_layers, n_kv_heads, head_dim, max_seq_len and device;
  * seq_len is not changed (call eakv_cache_advance on each).  The launch runs
- * on `stream` (NULL: caches[0]'s own) after the device-pointer calls already
- * enqueued on every named cache's own stream, and later work on those
- * streams (host-pointer calls included) runs after it. */
+ * on `stream` (NULL: the shared stream) after the device-pointer calls
+ * already enqueued there for every named cache, and later work on the shared
+ * stream and every later host-pointer call on a named cache run after it. */
 int eakv_append_batch_device(eakv_cache_t *const *caches, int n_caches,
                              const float *d_data, int n_tokens, void *stream);
 
@@ -92,11 +98,12 @@ int eakv_attention_fused(const eakv_cache_t *cache, const float *queries,
 
 /* Fused decode attention for n_caches same-shape caches (each over its own
  * seq_len) in one launch: d_q, d_out f32[n_caches][n_q][head_dim].  Uses the
- * workspace of caches[0].  The launch runs on `stream` (NULL: caches[0]'s
- * own) after the work already enqueued on every named cache's own stream
- * (device-pointer calls there, e.g. an append with a NULL stream).  It only
- * reads the other caches: work that later overwrites their tokens from
- * another stream must wait for `stream` first. */
+ * workspace of caches[0].  The launch runs on `stream` (NULL: the shared
+ * stream) after the work already enqueued there for every named cache
+ * (device-pointer calls with a NULL stream, e.g. an append); with a NULL
+ * stream, later host-pointer calls on any named cache run after it.  Work
+ * that later overwrites their tokens from a caller's stream must wait for
+ * `stream` first. */
 int eakv_attention_fused_batch_device(eakv_cache_t *const *caches,
                                       int n_caches, int layer,
                                       const float *d_q, int n_q_heads,
@@ -119,6 +126,19 @@ int eakv_attention_fused_batch_device_noalloc(eakv_cache_t *const *caches,
                                               const float *d_q, int n_q_heads,
                                               int n_kv_heads, float *d_out,
                                               void *stream);
+
+/* No counterpart in the reference (its fused kernel is one CPU loop).  The
+ * launch that eakv_attention_fused_batch_device (noalloc = 0) or its
+ * allocation-free form (noalloc != 0) makes for these caches at their
+ * current seq_len and this head split, for diagnostics and tests; nothing is
+ * launched.  plan (8 entries): [0] 1 for the matrix-core program, 0 for the
+ * VALU program (layer blocks beyond 32-bit buffer offsets); [1] chunks per
+ * (sequence, kv head) unit; [2] 1 when the chunks are merged inside the
+ * launch, 0 when a merge launch follows; [3] tokens per tile; [4] waves per
+ * block; [5] the most tiles one wave walks; [6] quads of q heads per wave;
+ * [7] virtual kv heads per kv head (groups above 8 q heads). */
+int eakv_attention_fused_plan(eakv_cache_t *const *caches, int n_caches, int n_q_heads,
+                              int n_kv_heads, int noalloc, int32_t *plan);
 
 /* Dequantize groups [group_start, group_start + group_count) of the (layer,
  * kv_idx) planes to f32, 64 values per group in group order: value =

@@ -36,3 +36,41 @@ def tol_close(got, want, atol=1e-4, rtol=1e-5):
     lim = atol + rtol * np.abs(want)
     bad = ~(err <= lim)
     return (not bad.any()), float(err.max(initial=0.0)), int(bad.sum())
+
+
+def check_against_reference(got, ref, exact, atol=1e-4, rtol=1e-5):
+    """The fused-attention bar: got within atol + rtol*|ref| of the reference
+    algorithm's result ref (the oracle's restatement of
+    fused_attention.ea:190-373).
+
+    Over long contexts with sharp softmax rows the reference's single f32
+    chain of softmax weights (fused_attention.ea:280-359) drops the terms
+    below half an ulp of its running sum, and a result closer to the exact
+    attention cannot meet that bar.  The exception is asserted, never
+    assumed: where got misses the bar against ref,
+      - ref itself misses the bar against exact (the f64 attention over the
+        same quantized cache) somewhere,
+      - got is within the bar of exact everywhere, and
+      - elementwise |got - ref| <= |ref - exact| + atol + rtol*|ref|
+        (got is no farther from the reference than the reference is from
+        the exact result, plus the bar).
+    Returns (mode, e_got_ref, e_ref_exact, e_got_exact): mode "reference"
+    when the plain bar holds, "exact" when the exception was taken."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    exact = np.asarray(exact, np.float64)
+    ok, e_gr, n_gr = tol_close(got, ref, atol, rtol)
+    e_re = float(np.abs(ref - exact).max(initial=0.0))
+    e_ge = float(np.abs(got - exact).max(initial=0.0))
+    if ok:
+        return "reference", e_gr, e_re, e_ge
+    ref_ok, _, n_re = tol_close(ref, exact, atol, rtol)
+    assert not ref_ok, (f"{n_gr} values miss the bar against the reference (max {e_gr}) "
+                        f"although the reference meets it against the exact result")
+    got_ok, _, n_ge = tol_close(got, exact, atol, rtol)
+    assert got_ok, (f"{n_ge} values miss the bar against the exact result (max {e_ge}); "
+                    f"reference {e_re} ({n_re} values outside)")
+    lim = np.abs(ref - exact) + atol + rtol * np.abs(ref)
+    over = np.abs(got - ref) > lim
+    assert not over.any(), (int(over.sum()), float((np.abs(got - ref) - lim).max()))
+    return "exact", e_gr, e_re, e_ge

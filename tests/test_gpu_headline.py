@@ -1,0 +1,215 @@
+"""The headline launch exactly as the benchmark times it, against the CPU
+oracle through the C ABI.
+
+The 32Q/8KV d128 32K-context workload's step: 8 sequences whose caches hold
+32767 tokens, one token appended to each by one batched append, then one
+eakv_attention_fused_batch_device call over all 8 caches (32 q heads, 8 kv
+heads, 32768 tokens each).  On MI355X's 256 CUs that launch has 64 units
+(sequence, kv head) of 8 chunks, merges its chunks inside the launch and
+walks 32 tiles of 32 tokens per wave; the plan is read back from the library
+(eakv_attention_fused_plan) and asserted, so the test checks the launch the
+benchmark runs and not a neighbour of it.  The allocation-free form of the
+same call (chunks merged by a second launch) must give the same bits.
+
+Each sequence is compared with the reference algorithm (the oracle's fused
+call, the AVX-512 restatement of fused_attention.ea:190-373 where the host
+has AVX-512) at 1e-4 abs / 1e-5 rel, with the long-context exception
+asserted by check_against_reference (the reference's f32 weight sum against
+the exact f64 attention over the same quantized cache).
+
+A second case runs single-quad waves through at least 16 tiles each at
+other shapes (16 kv heads, ragged contexts, d=64), with the chunks merged in
+the launch.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import check_against_reference, tol_close
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-4, 1e-5
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def E():
+    import eakv_amd
+    from eakv_amd import hipmem
+    if hipmem.device_count() < 1:
+        pytest.fail("no HIP device visible")
+    return eakv_amd
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def n_cu():
+    lib = C.CDLL(os.path.join(ROOT, "eakv_amd", "libeakv_synth.so"))
+    lib.eakv_synth_cu_count.restype = C.c_int
+    return lib.eakv_synth_cu_count() or 256
+
+
+def chan_k(rng, n_kv, L, d):
+    """K of the 32Q/8KV workload: N(0,1) times per-channel scales log-uniform
+    in [0.5, 4], two channels per head x10."""
+    ch = np.exp(rng.uniform(np.log(0.5), np.log(4.0), (n_kv, 1, d))).astype(np.float32)
+    for h in range(n_kv):
+        ch[h, 0, rng.choice(d, 2, replace=False)] *= 10
+    return rng.standard_normal((n_kv, L, d), dtype=np.float32) * ch
+
+
+def exact_attention(o, q, n_q, n_kv, L):
+    """softmax(q.K/sqrt(d)) V in f64 over layer 0 of the oracle cache's
+    quantized planes (K and V = nibble*scale + bias exactly)."""
+    nh, d, lmax = o.n_heads, o.head_dim, o.max_seq_len
+    kv = []
+    for k in (0, 1):
+        w, s, b = o.read_planes(0, k)
+        n = np.concatenate([w & 15, w >> 4], axis=1).astype(np.float64)
+        x = n * s.astype(np.float64)[:, None] + b.astype(np.float64)[:, None]
+        kv.append(x.reshape(nh, lmax, d)[:n_kv, :L])
+        del w, s, b, n, x
+    K, V = kv
+    qpk = n_q // n_kv
+    out = np.zeros((n_q, d))
+    for h in range(n_q):
+        sc = K[h // qpk] @ q[h].astype(np.float64) / np.sqrt(d)
+        p = np.exp(sc - sc.max())
+        out[h] = p @ V[h // qpk] / p.sum()
+    return out
+
+
+def build_batch(E, seed, n_seq, n_kv, d, lens, lmax, kdist):
+    """n_seq one-layer caches (GPU and oracle) of lens[i] tokens each, every
+    sequence seeded separately; K from kdist, V ~ N(0,1)."""
+    gs, os_ = [], []
+    for i in range(n_seq):
+        rng = np.random.default_rng(seed + 1000 * i)
+        L = lens[i]
+        K = kdist(rng, n_kv, L, d)
+        V = rng.standard_normal((n_kv, L, d), dtype=np.float32)
+        data = np.stack([K, V])
+        del K, V
+        g, o = E.Cache(1, n_kv, d, lmax), O.OracleCache(1, n_kv, d, lmax)
+        g.load_raw(data, L)
+        o.load_raw(data, L)
+        del data
+        gs.append(g)
+        os_.append(o)
+        say("  filled sequence", i, "tokens", L)
+    return gs, os_
+
+
+def batch_call(E, fn, gs, q, n_q, n_kv):
+    from eakv_amd.hipmem import DeviceArray
+    dq = DeviceArray.from_host(q)
+    dout = DeviceArray(q.shape)
+    say("  call", fn, "n_seq", len(gs))
+    assert getattr(E.lib(), fn)(E.handles(gs), len(gs), 0, dq.ptr, n_q, n_kv, dout.ptr,
+                                None) == 0, E.last_error()
+    gs[0].sync()
+    out = dout.download()
+    dq.free()
+    dout.free()
+    return out
+
+
+def compare_sequences(os_, q, out, n_q, n_kv, lens):
+    modes = []
+    for i, o in enumerate(os_):
+        ref = o.attention_fused_avx512(q[i], 0, n_q, n_kv) if O.avx512_available() \
+            else o.attention_fused(q[i], 0, n_q, n_kv)
+        exact = exact_attention(o, q[i], n_q, n_kv, lens[i])
+        mode, e_gr, e_re, e_ge = check_against_reference(out[i], ref, exact, ATOL, RTOL)
+        say(f"  sequence {i}: {mode} bar; gpu-reference {e_gr:.3g}, reference-exact "
+            f"{e_re:.3g}, gpu-exact {e_ge:.3g}")
+        modes.append(mode)
+    return modes
+
+
+def test_headline_launch_as_benchmarked(E):
+    """8 caches x 8 kv heads x 32768 tokens, 32 q heads, d=128: the
+    benchmark's batched append of token 32768 and its one fused launch, with
+    the launch plan asserted, both entry points, every sequence checked."""
+    n_seq, n_kv, n_q, d, L0 = 8, 8, 32, 128, 32767
+    lmax = L0 + 1 + 64                      # the benchmark's max_seq_len
+    say("headline: build", n_seq, "caches of", L0, "tokens")
+    gs, os_ = build_batch(E, 0xEA4B + 4, n_seq, n_kv, d, [L0] * n_seq, lmax, chan_k)
+    from eakv_amd.hipmem import DeviceArray
+    rng = np.random.default_rng(0xEA4B + 44)
+    tok = rng.standard_normal((n_seq, 1, 2, n_kv, 1, d), dtype=np.float32)
+    dtok = DeviceArray.from_host(tok)
+    say("headline: batched append of one token")
+    assert E.lib().eakv_append_batch_device(E.handles(gs), n_seq, dtok.ptr, 1, None) == 0
+    for i in range(n_seq):
+        gs[i].advance(1)
+        for kv in (0, 1):
+            os_[i].append(tok[i, 0, kv], 0, kv, 1)
+        os_[i].advance(1)
+    L = L0 + 1
+
+    plan = E.fused_plan(gs, n_q, n_kv)
+    say("headline: plan", plan)
+    cu = n_cu()
+    chunks = 2 * cu // (n_seq * n_kv)        # two one-quad blocks per CU, 64 units
+    assert plan["mfma"] == 1 and plan["quads"] == 1 and plan["split"] == 1
+    assert plan["waves_per_block"] == 4 and plan["tile_tokens"] == 32
+    assert plan["chunks"] == chunks
+    assert plan["merged_in_launch"] == 1
+    assert plan["tiles_per_wave"] == -(-(L // 32) // (chunks * 4))
+    if cu == 256:
+        assert (plan["chunks"], plan["tiles_per_wave"]) == (8, 32)
+    na_plan = E.fused_plan(gs, n_q, n_kv, noalloc=True)
+    assert na_plan["merged_in_launch"] == 0
+    assert {k: v for k, v in na_plan.items() if k != "merged_in_launch"} == \
+        {k: v for k, v in plan.items() if k != "merged_in_launch"}
+
+    q = rng.standard_normal((n_seq, n_q, d), dtype=np.float32)
+    out = batch_call(E, "eakv_attention_fused_batch_device", gs, q, n_q, n_kv)
+    out_na = batch_call(E, "eakv_attention_fused_batch_device_noalloc", gs, q, n_q, n_kv)
+    # the in-launch merge restates the merge launch's arithmetic and order
+    assert np.array_equal(out.view(np.uint32), out_na.view(np.uint32))
+    # a second call of the workspace form: the counters were left at zero
+    out2 = batch_call(E, "eakv_attention_fused_batch_device", gs, q, n_q, n_kv)
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+    compare_sequences(os_, q, out, n_q, n_kv, [L] * n_seq)
+    # the appended token is in the launch: K-scores of its position,
+    # bit-exact against the oracle for one sequence
+    s_g = gs[5].attention_scores(q[5], 0, n_q, n_kv)
+    s_o = os_[5].attention_scores(q[5], 0, n_q, n_kv)
+    assert np.array_equal(s_g.view(np.uint32), s_o.view(np.uint32))
+    dtok.free()
+    for g in gs:
+        g.free()
+
+
+@pytest.mark.parametrize("d,n_kv,n_q,lens", [
+    (128, 16, 64, [18000, 17001, 12345, 18000]),
+    (64, 16, 32, [30000, 29999, 4097, 1])])
+def test_single_quad_waves_many_tiles(E, d, n_kv, n_q, lens):
+    """Single-quad waves (up to 4 q heads per kv head) through at least 16
+    tiles each, chunks merged in the launch, ragged contexts in one batch
+    (the shorter sequences' waves run out of tiles early and their blocks
+    still count on the unit counters)."""
+    n_seq = len(lens)
+    say("many-tiles: build", d, n_kv, n_q, lens)
+    gs, os_ = build_batch(E, 0xEA4B + 77 + d, n_seq, n_kv, d, lens, max(lens) + 8, chan_k)
+    plan = E.fused_plan(gs, n_q, n_kv)
+    say("many-tiles: plan", plan)
+    assert plan["mfma"] == 1 and plan["quads"] == 1
+    assert plan["merged_in_launch"] == 1
+    assert plan["tiles_per_wave"] >= 16
+    rng = np.random.default_rng(0xEA4B + 78 + d)
+    q = rng.standard_normal((n_seq, n_q, d), dtype=np.float32)
+    out = batch_call(E, "eakv_attention_fused_batch_device", gs, q, n_q, n_kv)
+    out_na = batch_call(E, "eakv_attention_fused_batch_device_noalloc", gs, q, n_q, n_kv)
+    assert np.array_equal(out.view(np.uint32), out_na.view(np.uint32))
+    compare_sequences(os_, q, out, n_q, n_kv, lens)
+    for g in gs:
+        g.free()

@@ -367,18 +367,27 @@ def test_fused_rising_and_falling_scores(E, rng, d, n_q, n_kv, L, slope):
 def test_fused_huge_scores_as_accurate_as_reference(E, rng, d, n_q, n_kv, L, slope):
     """Scores in the thousands: one f32 ulp of a score (2.4e-4 at 3000) moves
     its weight by that much relative, so any two f32 orders of the score
-    arithmetic differ by more than the 1e-4 bar (the reference's own order is
-    3e-4 off the exact result here).  Held instead to the exact f64 attention
-    over the same quantized cache: the fused kernel within twice the
-    reference algorithm's error."""
+    arithmetic differ by more than the 1e-4 bar.  The exception is asserted:
+    the reference algorithm itself misses the bar against the exact f64
+    attention over the same quantized cache.  The fused kernel is then held
+    to the exact result: no farther from it than the reference algorithm,
+    at the largest error and value by value within the reference's error
+    plus the bar (which bounds its distance from the reference by twice the
+    reference's own error plus the bar)."""
     say("fused-huge", d, n_q, n_kv, L, slope)
     g, o, q, smax = slope_case(E, rng, d, n_q, n_kv, L, slope, center=False)
     assert smax > 700
     exact = exact_attention(o, q, 0, n_q, n_kv, L)
-    e_gpu = float(np.abs(g.attention_fused(q, 0, n_q, n_kv) - exact).max())
-    e_ref = float(np.abs(o.attention_fused(q, 0, n_q, n_kv) - exact).max())
-    say("  max|score|", smax, "error vs exact: gpu", e_gpu, "reference algorithm", e_ref)
-    assert e_gpu <= 2 * e_ref + 1e-5
+    got = g.attention_fused(q, 0, n_q, n_kv).astype(np.float64)
+    ref = o.attention_fused(q, 0, n_q, n_kv).astype(np.float64)
+    e_gpu = float(np.abs(got - exact).max())
+    e_ref = float(np.abs(ref - exact).max())
+    say("  max|score|", smax, "error vs exact: gpu", e_gpu, "reference algorithm", e_ref,
+        "gpu vs reference", float(np.abs(got - ref).max()))
+    ref_ok, _, _ = tol_close(ref, exact, ATOL, RTOL)
+    assert not ref_ok, "the reference algorithm meets the bar here: no exception to take"
+    assert e_gpu <= e_ref
+    assert np.all(np.abs(got - exact) <= e_ref + ATOL + RTOL * np.abs(exact))
 
 
 @pytest.mark.parametrize("d,n_q,n_kv,L,where", [(128, 32, 8, 700, "k"), (128, 16, 2, 300, "v"),

@@ -1,0 +1,135 @@
+"""The reference's threading contract, "All functions are thread-safe for
+distinct caches" (reference include/eakv.h:3), through the host-pointer C
+API on the GPU.
+
+Two threads each drive a cache of their own at the same time (ctypes releases
+the GIL for the library's calls, so the calls overlap): load_raw, appends of
+every layer, advance, K-scores, the caller's softmax and the V-sum, the fused
+call, checkpoint and restore, round after round.  Each thread checks its
+results against an oracle cache of its own: planes and K-scores bit-exact,
+V-sum and fused outputs within 1e-4 abs / 1e-5 rel.  A third thread keeps the
+device's shared stream busy with device-pointer calls on a third cache,
+which the host-pointer calls of the other two must not wait for.
+"""
+import threading
+import time
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import tol_close
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-4, 1e-5
+
+
+@pytest.fixture(scope="module")
+def E():
+    import eakv_amd
+    from eakv_amd import hipmem
+    if hipmem.device_count() < 1:
+        pytest.fail("no HIP device visible")
+    return eakv_amd
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def drive(E, name, nl, nh, d, n_q, L0, n_new, rounds, seed, start, log):
+    rng = np.random.default_rng(seed)
+    lmax = L0 + rounds * n_new
+    g, o = E.Cache(nl, nh, d, lmax), O.OracleCache(nl, nh, d, lmax)
+    data = rng.standard_normal(nl * 2 * nh * L0 * d).astype(np.float32)
+    start.wait()
+    g.load_raw(data, L0)
+    o.load_raw(data, L0)
+    del data
+    for r in range(rounds):
+        for l in range(nl):
+            for kv in (0, 1):
+                x = rng.standard_normal((nh, n_new, d)).astype(np.float32)
+                g.append(x, l, kv, n_new)
+                o.append(x, l, kv, n_new)
+        g.advance(n_new)
+        o.advance(n_new)
+        layer = r % nl
+        for kv in (0, 1):
+            a, b = g.read_planes(layer, kv), o.read_planes(layer, kv)
+            assert all(np.array_equal(np.ascontiguousarray(x).view(np.uint8),
+                                      np.ascontiguousarray(y).view(np.uint8))
+                       for x, y in zip(a, b)), (name, r, kv)
+        q = rng.standard_normal((n_q, d)).astype(np.float32)
+        sg = g.attention_scores(q, layer, n_q, nh)
+        so = o.attention_scores(q, layer, n_q, nh)
+        assert np.array_equal(sg.view(np.uint32), so.view(np.uint32)), (name, r)
+        w = O.softmax_rows(so)
+        ok, err, nbad = tol_close(g.attention_output(w, layer, n_q, nh),
+                                  o.attention_output(w, layer, n_q, nh), ATOL, RTOL)
+        assert ok, (name, r, "output", err, nbad)
+        ok, err, nbad = tol_close(g.attention_fused(q, layer, n_q, nh),
+                                  o.attention_fused(q, layer, n_q, nh), ATOL, RTOL)
+        assert ok, (name, r, "fused", err, nbad)
+        # rewind half a round and append again (the next round overwrites)
+        cp = g.checkpoint()
+        assert cp == o.checkpoint()
+        g.restore(cp - n_new // 2)
+        o.restore(cp - n_new // 2)
+        log.append((name, r))
+    g.free()
+    o.free()
+
+
+def busy_shared_stream(E, stop, count):
+    """Device-pointer fused calls on a third cache, on the shared stream, until
+    stop is set (each waited for, so the queue stays short)."""
+    from eakv_amd.hipmem import DeviceArray
+    nh, d, n_q, L = 8, 128, 32, 60000
+    c = E.Cache(1, nh, d, L)
+    rng = np.random.default_rng(7)
+    c.load_raw(rng.standard_normal(2 * nh * L * d).astype(np.float32), L)
+    dq = DeviceArray.from_host(rng.standard_normal((1, n_q, d)).astype(np.float32))
+    dout = DeviceArray((1, n_q, d))
+    h = E.handles([c])
+    while not stop.is_set():
+        for _ in range(20):
+            assert E.lib().eakv_attention_fused_batch_device(h, 1, 0, dq.ptr, n_q, nh,
+                                                             dout.ptr, None) == 0
+        c.sync()
+        count[0] += 20
+    dq.free()
+    dout.free()
+    c.free()
+
+
+def test_distinct_caches_from_concurrent_threads(E):
+    specs = [("gqa-d128", 2, 8, 128, 32, 20000, 3000, 4, 101),
+             ("mha-d64", 3, 4, 64, 4, 30000, 2000, 4, 202)]
+    start = threading.Barrier(len(specs))
+    stop = threading.Event()
+    count = [0]
+    errors, log = [], []
+
+    def run(spec):
+        try:
+            drive(E, *spec, start, log)
+        except BaseException as e:      # re-raised in the main thread
+            errors.append((spec[0], e))
+
+    busy = threading.Thread(target=busy_shared_stream, args=(E, stop, count))
+    busy.start()
+    threads = [threading.Thread(target=run, args=(s,)) for s in specs]
+    t0 = time.perf_counter()
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    stop.set()
+    busy.join()
+    say("threads: rounds", log, "in", round(time.perf_counter() - t0, 2), "s; fused calls "
+        "on the shared stream meanwhile:", count[0])
+    if errors:
+        raise errors[0][1]
+    assert sorted(log) == sorted((s[0], r) for s in specs for r in range(s[7]))

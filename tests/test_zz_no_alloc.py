@@ -95,3 +95,49 @@ def test_noalloc_rejects_launch_beyond_scratch(E):
                                                           128, dout.ptr, None)
     assert rc == E.EAKV_ERR_INVALID
     assert b"scratch" in E.lib().eakv_last_error_message()
+
+
+def test_noalloc_after_null_stream_batch_append(E, rng):
+    """A batched append on the shared stream (NULL) writes caches c0, c1 and
+    c2.  The allocation-free call over [c1, c2] on a caller's stream right
+    behind it must run after it (the append is pending work of every cache
+    it names, not of c0 alone), and so must the workspace form on another
+    caller's stream and a host-pointer call on c2 (the cache's own stream)."""
+    from eakv_amd.hipmem import DeviceArray, Stream
+    nh, d, n_q, n_new = 4, 128, 16, 6000
+    gs, os_ = caches(E, rng, 1, nh, d, [2000, 3000, 2500], 2000 + 3000 + n_new)
+    x = rng.standard_normal((3, 1, 2, nh, n_new, d)).astype(np.float32)
+    dx = DeviceArray.from_host(x)
+    say("race: batched append on the shared stream")
+    assert E.lib().eakv_append_batch_device(E.handles(gs), 3, dx.ptr, n_new, None) == 0
+    for i in range(3):
+        gs[i].advance(n_new)
+        for kv in (0, 1):
+            os_[i].append(x[i, 0, kv], 0, kv, n_new)
+        os_[i].advance(n_new)
+    q = rng.standard_normal((2, n_q, d)).astype(np.float32)
+    dq = DeviceArray.from_host(q)
+    outs = []
+    for fn in ("eakv_attention_fused_batch_device_noalloc", "eakv_attention_fused_batch_device"):
+        st = Stream()
+        dout = DeviceArray((2, n_q, d))
+        say("race:", fn, "on a caller's stream")
+        assert getattr(E.lib(), fn)(E.handles(gs[1:]), 2, 0, dq.ptr, n_q, nh, dout.ptr,
+                                    st.s) == 0, E.last_error()
+        st.synchronize()
+        outs.append(dout.download())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    for i in range(2):
+        ok, err, nbad = tol_close(outs[0][i], os_[i + 1].attention_fused(q[i], 0, n_q, nh))
+        assert ok, (i, err, nbad)
+    # another append on the shared stream, then a host-pointer call on c2
+    x2 = rng.standard_normal((3, 1, 2, nh, 500, d)).astype(np.float32)
+    dx2 = DeviceArray.from_host(x2)
+    assert E.lib().eakv_append_batch_device(E.handles(gs), 3, dx2.ptr, 500, None) == 0
+    gs[2].advance(500)
+    for kv in (0, 1):
+        os_[2].append(x2[2, 0, kv], 0, kv, 500)
+    os_[2].advance(500)
+    a = gs[2].attention_scores(q[1], 0, n_q, nh)
+    b = os_[2].attention_scores(q[1], 0, n_q, nh)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
