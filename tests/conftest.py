@@ -45,32 +45,44 @@ def check_against_reference(got, ref, exact, atol=1e-4, rtol=1e-5):
 
     Over long contexts with sharp softmax rows the reference's single f32
     chain of softmax weights (fused_attention.ea:280-359) drops the terms
-    below half an ulp of its running sum, and a result closer to the exact
-    attention cannot meet that bar.  The exception is asserted, never
-    assumed: where got misses the bar against ref,
-      - ref itself misses the bar against exact (the f64 attention over the
-        same quantized cache) somewhere,
-      - got is within the bar of exact everywhere, and
-      - elementwise |got - ref| <= |ref - exact| + atol + rtol*|ref|
-        (got is no farther from the reference than the reference is from
-        the exact result, plus the bar).
-    Returns (mode, e_got_ref, e_ref_exact, e_got_exact): mode "reference"
-    when the plain bar holds, "exact" when the exception was taken."""
+    below half an ulp of its running sum; its outputs then sit up to and
+    beyond the bar away from the exact attention, and a result closer to the
+    exact one can miss the bar against the reference.  That exception is
+    checked value by value, never assumed: at every value where got misses
+    the bar against ref,
+      - got is closer to exact (the f64 attention over the same quantized
+        cache) than ref is, so the reference's own error is what puts the
+        two apart (and that error is then above half the bar there);
+    and everywhere
+      - got is within the bar of exact, and
+      - |got - ref| <= |ref - exact| + atol + rtol*|ref|.
+    Returns (mode, e_got_ref, e_ref_exact, e_got_exact, n_excused, ref_bar):
+    mode "reference" when the plain bar holds, "exact" when the exception
+    was taken for n_excused values; ref_bar is the reference's largest error
+    against exact as a fraction of the bar."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     exact = np.asarray(exact, np.float64)
-    ok, e_gr, n_gr = tol_close(got, ref, atol, rtol)
-    e_re = float(np.abs(ref - exact).max(initial=0.0))
-    e_ge = float(np.abs(got - exact).max(initial=0.0))
-    if ok:
-        return "reference", e_gr, e_re, e_ge
-    ref_ok, _, n_re = tol_close(ref, exact, atol, rtol)
-    assert not ref_ok, (f"{n_gr} values miss the bar against the reference (max {e_gr}) "
-                        f"although the reference meets it against the exact result")
-    got_ok, _, n_ge = tol_close(got, exact, atol, rtol)
-    assert got_ok, (f"{n_ge} values miss the bar against the exact result (max {e_ge}); "
-                    f"reference {e_re} ({n_re} values outside)")
-    lim = np.abs(ref - exact) + atol + rtol * np.abs(ref)
-    over = np.abs(got - ref) > lim
-    assert not over.any(), (int(over.sum()), float((np.abs(got - ref) - lim).max()))
-    return "exact", e_gr, e_re, e_ge
+    d_gr = np.abs(got - ref)
+    d_re = np.abs(ref - exact)
+    d_ge = np.abs(got - exact)
+    bar_ref = atol + rtol * np.abs(ref)
+    bar_ex = atol + rtol * np.abs(exact)
+    e_gr, e_re, e_ge = (float(x.max(initial=0.0)) for x in (d_gr, d_re, d_ge))
+    ref_bar = float((d_re / bar_ex).max(initial=0.0))
+    over = ~(d_gr <= bar_ref)
+    if not over.any():
+        return "reference", e_gr, e_re, e_ge, 0, ref_bar
+    idx = tuple(np.argwhere(over)[0])
+    where = (f"first at {idx}: got {got[idx]!r}, reference {ref[idx]!r}, "
+             f"exact {exact[idx]!r}")
+    closer = d_ge[over] < d_re[over]
+    assert closer.all(), (f"{int((~closer).sum())} of {int(over.sum())} values that miss "
+                          f"the bar against the reference are not closer to the exact "
+                          f"result than the reference is; {where}")
+    within = d_ge <= bar_ex
+    assert within.all(), (f"{int((~within).sum())} values miss the bar against the exact "
+                          f"result (max {e_ge}); {where}")
+    lim = d_re + bar_ref
+    assert (d_gr <= lim).all(), float((d_gr - lim).max())
+    return "exact", e_gr, e_re, e_ge, int(over.sum()), ref_bar

@@ -23,6 +23,7 @@ the launch.
 """
 import ctypes as C
 import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -85,24 +86,35 @@ def exact_attention(o, q, n_q, n_kv, L):
     return out
 
 
+# worker threads for the per-sequence CPU work (numpy's generators and the
+# oracle library release the GIL)
+POOL = 8
+
+
 def build_batch(E, seed, n_seq, n_kv, d, lens, lmax, kdist):
     """n_seq one-layer caches (GPU and oracle) of lens[i] tokens each, every
-    sequence seeded separately; K from kdist, V ~ N(0,1)."""
-    gs, os_ = [], []
-    for i in range(n_seq):
+    sequence seeded separately; K from kdist, V ~ N(0,1).  The inputs are
+    drawn and the oracle caches filled on worker threads, the GPU caches
+    loaded in order as their inputs arrive."""
+    def make(i):
         rng = np.random.default_rng(seed + 1000 * i)
         L = lens[i]
-        K = kdist(rng, n_kv, L, d)
-        V = rng.standard_normal((n_kv, L, d), dtype=np.float32)
-        data = np.stack([K, V])
-        del K, V
-        g, o = E.Cache(1, n_kv, d, lmax), O.OracleCache(1, n_kv, d, lmax)
-        g.load_raw(data, L)
+        data = np.empty((2, n_kv, L, d), np.float32)
+        data[0] = kdist(rng, n_kv, L, d)
+        data[1] = rng.standard_normal((n_kv, L, d), dtype=np.float32)
+        o = O.OracleCache(1, n_kv, d, lmax)
         o.load_raw(data, L)
-        del data
-        gs.append(g)
-        os_.append(o)
-        say("  filled sequence", i, "tokens", L)
+        return data, o
+
+    gs, os_ = [], []
+    with ThreadPoolExecutor(POOL) as ex:
+        for i, (data, o) in enumerate(ex.map(make, range(n_seq))):
+            g = E.Cache(1, n_kv, d, lmax)
+            g.load_raw(data, lens[i])
+            del data
+            gs.append(g)
+            os_.append(o)
+            say("  filled sequence", i, "tokens", lens[i])
     return gs, os_
 
 
@@ -121,15 +133,23 @@ def batch_call(E, fn, gs, q, n_q, n_kv):
 
 
 def compare_sequences(os_, q, out, n_q, n_kv, lens):
-    modes = []
-    for i, o in enumerate(os_):
+    """Every sequence against the reference algorithm and the exact result
+    (computed on worker threads), checked in order."""
+    def refs(i):
+        o = os_[i]
         ref = o.attention_fused_avx512(q[i], 0, n_q, n_kv) if O.avx512_available() \
             else o.attention_fused(q[i], 0, n_q, n_kv)
-        exact = exact_attention(o, q[i], n_q, n_kv, lens[i])
-        mode, e_gr, e_re, e_ge = check_against_reference(out[i], ref, exact, ATOL, RTOL)
-        say(f"  sequence {i}: {mode} bar; gpu-reference {e_gr:.3g}, reference-exact "
-            f"{e_re:.3g}, gpu-exact {e_ge:.3g}")
-        modes.append(mode)
+        return ref, exact_attention(o, q[i], n_q, n_kv, lens[i])
+
+    modes = []
+    with ThreadPoolExecutor(POOL) as ex:
+        for i, (ref, exact) in enumerate(ex.map(refs, range(len(os_)))):
+            mode, e_gr, e_re, e_ge, n_ex, ref_bar = check_against_reference(
+                out[i], ref, exact, ATOL, RTOL)
+            say(f"  sequence {i}: {mode} bar; gpu-reference {e_gr:.3g}, reference-exact "
+                f"{e_re:.3g} ({ref_bar:.3f} of the bar), gpu-exact {e_ge:.3g}, "
+                f"{n_ex} values excused")
+            modes.append(mode)
     return modes
 
 

@@ -365,28 +365,32 @@ def test_fused_rising_and_falling_scores(E, rng, d, n_q, n_kv, L, slope):
 @pytest.mark.parametrize("d,n_q,n_kv,L,slope", [(128, 64, 8, 2000, 1.5),
                                                (128, 32, 8, 3000, 0.25)])
 def test_fused_huge_scores_as_accurate_as_reference(E, rng, d, n_q, n_kv, L, slope):
-    """Scores in the thousands: one f32 ulp of a score (2.4e-4 at 3000) moves
-    its weight by that much relative, so any two f32 orders of the score
-    arithmetic differ by more than the 1e-4 bar.  The exception is asserted:
-    the reference algorithm itself misses the bar against the exact f64
-    attention over the same quantized cache.  The fused kernel is then held
-    to the exact result: no farther from it than the reference algorithm,
-    at the largest error and value by value within the reference's error
-    plus the bar (which bounds its distance from the reference by twice the
-    reference's own error plus the bar)."""
+    """Scores in the hundreds and thousands: one f32 ulp of the largest score
+    (6.1e-5 at 788, 2.4e-4 at 3203) moves its token's weight by that much
+    relative, and so the outputs by more than the 1e-4 bar; two f32 orders
+    of the score arithmetic (the reference's fma chain, the fused kernel's
+    exact integer dots recombined in f32) cannot agree within the bar, nor
+    either of them meet it against the exact f64 attention over the same
+    quantized cache.  The premise is asserted (ulp(max|score|) * max|output|
+    above the bar), and the fused kernel is held to the exact result: no less
+    accurate than the reference algorithm at the largest error and in the
+    mean square, and value by value within the reference's largest error
+    plus the bar."""
     say("fused-huge", d, n_q, n_kv, L, slope)
     g, o, q, smax = slope_case(E, rng, d, n_q, n_kv, L, slope, center=False)
     assert smax > 700
     exact = exact_attention(o, q, 0, n_q, n_kv, L)
+    assert float(np.spacing(np.float32(smax))) * float(np.abs(exact).max()) > ATOL
     got = g.attention_fused(q, 0, n_q, n_kv).astype(np.float64)
     ref = o.attention_fused(q, 0, n_q, n_kv).astype(np.float64)
     e_gpu = float(np.abs(got - exact).max())
     e_ref = float(np.abs(ref - exact).max())
-    say("  max|score|", smax, "error vs exact: gpu", e_gpu, "reference algorithm", e_ref,
-        "gpu vs reference", float(np.abs(got - ref).max()))
-    ref_ok, _, _ = tol_close(ref, exact, ATOL, RTOL)
-    assert not ref_ok, "the reference algorithm meets the bar here: no exception to take"
+    r_gpu = float(np.sqrt(np.mean((got - exact) ** 2)))
+    r_ref = float(np.sqrt(np.mean((ref - exact) ** 2)))
+    say("  max|score|", smax, "error vs exact (max, rms): gpu", e_gpu, r_gpu,
+        "reference algorithm", e_ref, r_ref, "gpu vs reference", float(np.abs(got - ref).max()))
     assert e_gpu <= e_ref
+    assert r_gpu <= r_ref
     assert np.all(np.abs(got - exact) <= e_ref + ATOL + RTOL * np.abs(exact))
 
 
