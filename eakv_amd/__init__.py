@@ -286,7 +286,7 @@ def handles(caches):
     return arr
 
 
-FUSED_PLAN_KEYS = ("mfma", "chunks", "merged_in_launch", "tile_tokens", "waves_per_block",
+FUSED_PLAN_KEYS = ("mfma", "chunks", "merge_levels", "tile_tokens", "waves_per_block",
                    "tiles_per_wave", "quads", "split")
 
 

@@ -134,7 +134,8 @@ int eakv_attention_fused_batch_device_noalloc(eakv_cache_t *const *caches,
  * launched.  plan (8 entries): [0] 1 for the matrix-core program, 0 for the
  * VALU program (layer blocks beyond 32-bit buffer offsets); [1] chunks per
  * (sequence, kv head) unit; [2] 1 when the chunks are merged inside the
- * launch, 0 when a merge launch follows; [3] tokens per tile; [4] waves per
+ * launch (up to 16 chunks per unit), 0 when a merge launch follows; [3]
+ * tokens per tile; [4] waves per
  * block; [5] the most tiles one wave walks; [6] quads of q heads per wave;
  * [7] virtual kv heads per kv head (groups above 8 q heads). */
 int eakv_attention_fused_plan(eakv_cache_t *const *caches, int n_caches, int n_q_heads,

@@ -181,14 +181,14 @@ def test_headline_launch_as_benchmarked(E):
     assert plan["mfma"] == 1 and plan["quads"] == 1 and plan["split"] == 1
     assert plan["waves_per_block"] == 4 and plan["tile_tokens"] == 32
     assert plan["chunks"] == chunks
-    assert plan["merged_in_launch"] == 1
+    assert plan["merge_levels"] == 1
     assert plan["tiles_per_wave"] == -(-(L // 32) // (chunks * 4))
     if cu == 256:
         assert (plan["chunks"], plan["tiles_per_wave"]) == (8, 32)
     na_plan = E.fused_plan(gs, n_q, n_kv, noalloc=True)
-    assert na_plan["merged_in_launch"] == 0
-    assert {k: v for k, v in na_plan.items() if k != "merged_in_launch"} == \
-        {k: v for k, v in plan.items() if k != "merged_in_launch"}
+    assert na_plan["merge_levels"] == 0
+    assert {k: v for k, v in na_plan.items() if k != "merge_levels"} == \
+        {k: v for k, v in plan.items() if k != "merge_levels"}
 
     q = rng.standard_normal((n_seq, n_q, d), dtype=np.float32)
     out = batch_call(E, "eakv_attention_fused_batch_device", gs, q, n_q, n_kv)
@@ -223,7 +223,7 @@ def test_single_quad_waves_many_tiles(E, d, n_kv, n_q, lens):
     plan = E.fused_plan(gs, n_q, n_kv)
     say("many-tiles: plan", plan)
     assert plan["mfma"] == 1 and plan["quads"] == 1
-    assert plan["merged_in_launch"] == 1
+    assert plan["merge_levels"] == 1
     assert plan["tiles_per_wave"] >= 16
     rng = np.random.default_rng(0xEA4B + 78 + d)
     q = rng.standard_normal((n_seq, n_q, d), dtype=np.float32)
@@ -233,3 +233,96 @@ def test_single_quad_waves_many_tiles(E, d, n_kv, n_q, lens):
     compare_sequences(os_, q, out, n_q, n_kv, lens)
     for g in gs:
         g.free()
+
+
+def chan_outlier_kv(rng, L, d):
+    """One kv head's K or V of the 70B-shape workload: N(0,1) times
+    per-channel scales log-uniform in [0.25, 8], 1% of the values +-20."""
+    ch = np.exp(rng.uniform(np.log(0.25), np.log(8.0), (1, d))).astype(np.float32)
+    x = rng.standard_normal((L, d), dtype=np.float32) * ch
+    m = rng.random(x.shape, dtype=np.float32) < 0.01
+    x[m] = np.where(rng.random(int(m.sum())) < 0.5, -20.0, 20.0).astype(np.float32)
+    return x
+
+
+def exact_attention_by_head(o, q, n_q, n_kv, L):
+    """exact_attention with one worker per kv head."""
+    d, lmax = o.head_dim, o.max_seq_len
+    planes = [o.read_planes(0, k) for k in (0, 1)]
+    gph = lmax * d // 64
+    qpk = n_q // n_kv
+
+    def head(kv):
+        KV = []
+        for w, s, b in planes:
+            sl = slice(kv * gph, kv * gph + L * d // 64)
+            n = np.concatenate([w[sl] & 15, w[sl] >> 4], axis=1).astype(np.float64)
+            KV.append((n * s[sl].astype(np.float64)[:, None] +
+                       b[sl].astype(np.float64)[:, None]).reshape(L, d))
+        K, V = KV
+        res = []
+        for h in range(kv * qpk, (kv + 1) * qpk):
+            sc = K @ q[h].astype(np.float64) / np.sqrt(d)
+            p = np.exp(sc - sc.max())
+            res.append(p @ V / p.sum())
+        return res
+
+    with ThreadPoolExecutor(POOL) as ex:
+        return np.array([r for rs in ex.map(head, range(n_kv)) for r in rs])
+
+
+def test_70b_shape_launch(E):
+    """One layer of the 70B-shape workload: 64 q heads / 8 kv heads, d=128,
+    131072 tokens, its K and V distribution.  On 256 CUs the launch runs
+    two-quad waves over 64-token tiles, 32 chunks per kv head, merged by a
+    second launch (merge_parts_kernel: 8 parts of 4 chunks, then the
+    parts); the allocation-free form and the host-pointer call must give the
+    same bits, and the result meets the reference bar, with the exception
+    checked value by value.  The V-sum of the oracle's softmax rows runs the
+    same chunks in V-sum mode against the oracle."""
+    n_kv, n_q, d, L = 8, 64, 128, 131072
+    lmax = L + 64
+    say("70b-shape: build")
+
+    def make(kv):
+        rng = np.random.default_rng(0xEA4B + 5 + 100 * kv)
+        return chan_outlier_kv(rng, L, d), chan_outlier_kv(rng, L, d)
+
+    data = np.empty((2, n_kv, L, d), np.float32)
+    with ThreadPoolExecutor(POOL) as ex:
+        for kv, (k, v) in enumerate(ex.map(make, range(n_kv))):
+            data[0, kv], data[1, kv] = k, v
+    g, o = E.Cache(1, n_kv, d, lmax), O.OracleCache(1, n_kv, d, lmax)
+    g.load_raw(data, L)
+    o.load_raw(data, L)
+    del data
+    plan = E.fused_plan([g], n_q, n_kv)
+    say("70b-shape: plan", plan)
+    assert plan["mfma"] == 1 and plan["quads"] == 2 and plan["tile_tokens"] == 64
+    assert plan["waves_per_block"] == 8 and plan["split"] == 1
+    if n_cu() == 256:
+        assert plan["chunks"] == 32 and plan["merge_levels"] == 0
+    rng = np.random.default_rng(0xEA4B + 55)
+    q = rng.standard_normal((1, n_q, d), dtype=np.float32)
+    out = batch_call(E, "eakv_attention_fused_batch_device", [g], q, n_q, n_kv)
+    out_na = batch_call(E, "eakv_attention_fused_batch_device_noalloc", [g], q, n_q, n_kv)
+    assert np.array_equal(out.view(np.uint32), out_na.view(np.uint32))
+    out2 = g.attention_fused(q[0], 0, n_q, n_kv)
+    assert np.array_equal(out[0].view(np.uint32), out2.view(np.uint32))
+    ref = o.attention_fused_avx512(q[0], 0, n_q, n_kv) if O.avx512_available() \
+        else o.attention_fused(q[0], 0, n_q, n_kv)
+    exact = exact_attention_by_head(o, q[0], n_q, n_kv, L)
+    mode, e_gr, e_re, e_ge, n_ex, ref_bar = check_against_reference(out[0], ref, exact, ATOL,
+                                                                    RTOL)
+    say(f"70b-shape: {mode} bar; gpu-reference {e_gr:.3g}, reference-exact {e_re:.3g} "
+        f"({ref_bar:.3f} of the bar), gpu-exact {e_ge:.3g}, {n_ex} values excused")
+    say("70b-shape: V-sum")
+    avx = O.avx512_available()
+    w = O.softmax_rows(o.attention_scores_avx512(q[0], 0, n_q, n_kv) if avx
+                       else o.attention_scores(q[0], 0, n_q, n_kv))
+    want = o.attention_output_avx512(w, 0, n_q, n_kv) if avx \
+        else o.attention_output(w, 0, n_q, n_kv)
+    ok, err, nbad = tol_close(g.attention_output(w, 0, n_q, n_kv), want, ATOL, RTOL)
+    assert ok, (err, nbad)
+    g.free()
+    o.free()
