@@ -132,14 +132,15 @@ int eakvi_work_end(eakv_cache_t *c, void *st)
 
 void *eakvi_stream_or_default(const eakv_cache_t *c, void *s)
 {
-    if (s) return s;
+    /* the shared stream named explicitly (eakv_cache_stream) is the default */
+    if (s && s != c->stream) return s;
     ((eakv_cache_t *)c)->own_async++;
     return c->stream;
 }
 
 void *eakvi_batch_stream(eakv_cache_t *const *caches, int n, void *s)
 {
-    if (s) return s;
+    if (s && s != caches[0]->stream) return s;
     for (int i = 0; i < n; i++) caches[i]->own_async++;
     return caches[0]->stream;
 }

@@ -66,9 +66,9 @@ int  eakvi_work_end(eakv_cache_t *c, void *st);
 int  eakvi_order_before(eakv_cache_t *c, void *st);
 int  eakvi_order_after(eakv_cache_t *const *caches, int n, void *st);
 
-/* The stream a device-pointer call runs on: the caller's, or (NULL) the
- * device's shared stream, which the call then counts as pending work of the
- * cache on it. */
+/* The stream a device-pointer call runs on: the caller's, or (NULL, or the
+ * shared stream named explicitly) the device's shared stream, which the call
+ * then counts as pending work of the cache on it. */
 void *eakvi_stream_or_default(const eakv_cache_t *c, void *s);
 /* The same for a call that names the caches [0, n): with a NULL stream the
  * launch is counted as pending work of every one of them. */

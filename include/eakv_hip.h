@@ -4,10 +4,10 @@
  * memory.  They exist because the reference API takes host pointers, which
  * forces a PCIe round trip per call on a GPU:
  *   - device-pointer forms of load/append/scores/output, asynchronous on a
- *     HIP stream (pass the hipStream_t as void*; NULL = the device's shared
- *     stream: one non-blocking stream per device, shared by every cache
- *     created on that device, so the device's caches' default-stream work
- *     runs in enqueue order);
+ *     HIP stream (pass the hipStream_t as void*; NULL, or eakv_cache_stream()
+ *     itself = the device's shared stream: one non-blocking stream per
+ *     device, shared by every cache created on that device, so the device's
+ *     caches' default-stream work runs in enqueue order);
  *   - batched append and batched fused decode attention over several caches
  *     of the same shape (one launch per layer for all sequences);
  *   - the fused single-pass softmax attention, which the reference compiles

@@ -133,3 +133,34 @@ def test_distinct_caches_from_concurrent_threads(E):
     if errors:
         raise errors[0][1]
     assert sorted(log) == sorted((s[0], r) for s in specs for r in range(s[7]))
+
+
+@pytest.mark.parametrize("explicit", [False, True])
+def test_host_call_after_device_append_on_shared_stream(E, explicit):
+    """A device-pointer append on the shared stream (NULL, or the stream
+    eakv_cache_stream returns, named explicitly) is pending work of the
+    cache: the next host-pointer call, which runs on the cache's own stream,
+    waits for it on the device and sees the appended tokens."""
+    from eakv_amd.hipmem import DeviceArray
+    nh, d, n_q, L0, n_new = 8, 128, 32, 3000, 20000
+    rng = np.random.default_rng(11 + explicit)
+    g, o = E.Cache(1, nh, d, L0 + n_new), O.OracleCache(1, nh, d, L0 + n_new)
+    data = rng.standard_normal(2 * nh * L0 * d).astype(np.float32)
+    g.load_raw(data, L0)
+    o.load_raw(data, L0)
+    st = g.stream if explicit else None
+    keep = []
+    for kv in (0, 1):
+        x = rng.standard_normal((nh, n_new, d)).astype(np.float32)
+        dx = DeviceArray.from_host(x)
+        keep.append(dx)
+        assert E.lib().eakv_cache_append_device(g.h, dx.ptr, 0, kv, n_new, st) == 0
+        o.append(x, 0, kv, n_new)
+    g.advance(n_new)
+    o.advance(n_new)
+    q = rng.standard_normal((n_q, d)).astype(np.float32)
+    a = g.attention_scores(q, 0, n_q, nh)
+    b = o.attention_scores(q, 0, n_q, nh)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    g.free()
+    o.free()
