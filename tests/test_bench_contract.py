@@ -93,3 +93,15 @@ def test_queued_timing_gives_up_after_four_holds(fake_synth, monkeypatch):
     with pytest.raises(RuntimeError, match="outlasted"):
         bench.timed(_FakeH, None, fn, steps=4, warmup=0, per=1, queued=True)
     assert len(fake_synth.holds) == 4
+
+
+def test_grow_steps_bounded_by_the_spare_tokens():
+    """The growing-context workload's caches hold 64 spare tokens: --grow-steps
+    outside 1..64 is refused before anything runs; --progress is accepted."""
+    for bad in ("0", "65"):
+        r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--grow-steps", bad],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 2 and "grow-steps" in r.stderr, (bad, r.stderr)
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--help"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "--progress" in r.stdout and "--grow-steps" in r.stdout
