@@ -1123,13 +1123,18 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             __builtin_amdgcn_sched_barrier(0);
             load_group(std::integral_constant<int, r + kSlots>{}, tk[kSlots - 1], tk[kSlots]);
             vsum(R);
-            // K(T(i+1)): scales, then bytes (the compiler waits for those)
-            Scales<D, TT> C;
+            // K(T(i+1)): scales, then bytes (the compiler waits for those).
+            // Past the unit's last tile there is none: its scores would all
+            // be masked (weights 0, no state change), so the wave's last
+            // iteration ends with V(T(i)).
             wait_vm<NKL + kLater>();
-            read_scales<D, TT>(sslot(std::integral_constant<int, (r + 1) % kSlots>{}), tl, C);
-            if constexpr (VS) vs_weights(st[(r + 1) % kSlots], C, tk[1] * TT);
-            else kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * TT);
             const bool more = tk[1] < n_tiles;
+            if (more) {
+                Scales<D, TT> C;
+                read_scales<D, TT>(sslot(std::integral_constant<int, (r + 1) % kSlots>{}), tl, C);
+                if constexpr (VS) vs_weights(st[(r + 1) % kSlots], C, tk[1] * TT);
+                else kscores_softmax(st[(r + 1) % kSlots], C, tk[1] * TT);
+            }
 #pragma unroll
             for (int j = 0; j < kSlots; j++) tk[j] = __builtin_amdgcn_readfirstlane(tk[j + 1]);
             return more;
