@@ -92,9 +92,12 @@ __device__ __forceinline__ void k_score_body(
     const uint8_t *hw = kw + hb * 32;
     const float *hs = ks + hb, *hbi = kb + hb;
     const float *qk = q + (int64_t)kvh * qpk * D;
+    // blockIdx.z: which of gridDim.z equal parts of the group's q heads
+    // this block dots (a grid too small for the chip splits the heads)
+    const int qn = qpk / (int)gridDim.z, o0 = (int)blockIdx.z * qn;
 
     // one 256-token slice: dequantize each lane's token once, then dot it
-    // with every q head of the kv head
+    // with every q head of the kv head in this block's part
     auto compute = [&](const KTok<D> &T, int sl) {
         const int t = sl * 256 + threadIdx.x;
         if constexpr (MHA) {
@@ -151,7 +154,7 @@ __device__ __forceinline__ void k_score_body(
                     dequant4<3>(klo, khi, lo, hi, T.sc[grp], T.bi[grp]);
                 }
             }
-        for (int o = 0; o < qpk; o++) {
+        for (int o = o0; o < o0 + qn; o++) {
             const float *qv = qk + (int64_t)o * D;
             float acc[16];
 #pragma unroll
@@ -216,6 +219,20 @@ int k_blocks(int n_sl, int n_kv)
     return want < n_sl ? want : n_sl;
 }
 
+// Parts of a group's q heads, one per block (gridDim.z): where the slices
+// alone leave the chip's resident blocks unfilled (short contexts, few kv
+// heads), the largest divisor of qpk that still fits, so each lane dots
+// fewer heads (each part dequantizes its tokens again, from L2).  32Q/4KV
+// d64 at 4096 tokens: 8 parts, 512 blocks instead of 64.
+int k_head_parts(int qpk, int blocks, int n_kv)
+{
+    const int64_t room = (int64_t)kKsBlocksPerCU * cu_count();
+    int hp = 1;
+    for (int d = 2; d <= qpk; d++)
+        if (qpk % d == 0 && (int64_t)n_kv * blocks * d <= room) hp = d;
+    return hp;
+}
+
 }  // namespace
 
 extern "C" int eakvd_k_score(const eakvd_geom *g, const uint8_t *base,
@@ -225,8 +242,9 @@ extern "C" int eakvd_k_score(const eakvd_geom *g, const uint8_t *base,
     if (seq_len <= 0) return 0;
     const Planes p = planes_of(*g, base, layer, 0);
     const hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((unsigned)k_blocks(ceil_div_i(seq_len, 256), n_kv), (unsigned)n_kv);
     const int qpk = n_q / n_kv;
+    const int kb = k_blocks(ceil_div_i(seq_len, 256), n_kv);
+    const dim3 grid((unsigned)kb, (unsigned)n_kv, (unsigned)k_head_parts(qpk, kb, n_kv));
     const float rs = 1.0f / sqrtf((float)g->head_dim);
     auto kern = g->head_dim == 64 ? (qpk == 1 ? k_score_mha_kernel<64> : k_score_kernel<64>)
                                   : (qpk == 1 ? k_score_mha_kernel<128> : k_score_kernel<128>);
