@@ -16,7 +16,10 @@
 // several 256-token slices with the next slice's loads in flight while it
 // computes the current one.  Nibbles become floats by masking a dword to four
 // byte-wide nibbles and converting its bytes (v_cvt_f32_ubyte0..3): exact,
-// as the reference's int-to-float conversion of the nibble.
+// as the reference's int-to-float conversion of the nibble.  Grids that
+// leave the chip unfilled split the work further: a group's q heads over
+// blocks, or (one q head per kv head) a token's 16 accumulators over four
+// lanes (k_score_mha4_kernel).
 #include "common.h"
 
 namespace {
@@ -199,7 +202,8 @@ __global__ __launch_bounds__(256) void k_score_kernel(
     k_score_body<D, false>(kw, ks, kb, gph, L, q, qpk, scores, rs);
 }
 
-// One q head per kv head: registers for 2 waves per SIMD.
+// One q head per kv head, one lane per token: registers for 2 waves per
+// SIMD.  Long contexts: its 16-byte loads read a token's row at once.
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_score_mha_kernel(
@@ -208,6 +212,130 @@ void k_score_mha_kernel(
     const float *__restrict__ q, int qpk, float *__restrict__ scores, float rs)
 {
     k_score_body<D, true>(kw, ks, kb, gph, L, q, qpk, scores, rs);
+}
+
+// One q head per kv head (MHA), short contexts: four lanes per token.  Lane part j of a
+// token runs the reference's accumulators 4j..4j+3 (acc_i: the fma chain,
+// in chunk order, of k[c*16+i] * q[c*16+i] with k = fma(nibble, scale,
+// bias)), so a lane does a quarter of a token's arithmetic and a slice's
+// last tokens cost a quarter of the time after their data land.  The
+// reference's pairwise halving tree (reduce16) is taken across the four
+// lanes by quad permutes: v8 = a + a of the lane two over, v4 = v8 + v8 of
+// the neighbour, then v2 and v1 in the lane; lane 0 of a token adds in the
+// reference's operand order, so scores stay bit-exact.  A block-slice is 64
+// tokens; lane j reads dword j of each 16-byte half of the token's groups.
+constexpr int kMhaBufs = 4;                         // slices per wave in flight, one consumed
+
+template <int D>
+struct KQuad {
+    uint32_t w[2 * (D / 64)];                       // dword j of (group, half)
+    float sc[D / 64], bi[D / 64];
+};
+
+template <int D>
+__device__ __forceinline__ void kq_load(const uint8_t *w, const float *sc, const float *bi,
+                                        int L, int sl, int ts, int j, KQuad<D> &T)
+{
+    constexpr int GPD = D / 64;
+    const int64_t t0 = (int64_t)sl * 64;
+    const int64_t left = L > t0 ? L - t0 : 0;       // tokens in this slice and after
+    const int nt = (int)(left < 64 ? left : 64);
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w + t0 * GPD * 32),
+                                                      (short)0, nt * GPD * 32, 0x00020000);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(sc + t0 * GPD),
+                                                      (short)0, nt * GPD * 4, 0x00020000);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(bi + t0 * GPD),
+                                                      (short)0, nt * GPD * 4, 0x00020000);
+#pragma unroll
+    for (int g = 0; g < GPD; g++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            T.w[2 * g + h] = __builtin_amdgcn_raw_buffer_load_b32(
+                rw, ts * GPD * 32 + g * 32 + h * 16 + 4 * j, 0, 0);
+#pragma unroll
+    for (int g = 0; g < GPD; g++) {
+        T.sc[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (ts * GPD + g) * 4, 0, 0));
+        T.bi[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, (ts * GPD + g) * 4, 0, 0));
+    }
+}
+
+// the value of lane (l ^ 2) and of lane (l ^ 1) within each quad of lanes
+__device__ __forceinline__ float quad_xor2(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float quad_xor1(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_score_mha4_kernel(
+    const uint8_t *__restrict__ kw, const float *__restrict__ ks,
+    const float *__restrict__ kb, int64_t gph, int L,
+    const float *__restrict__ q, float *__restrict__ scores, float rs)
+{
+    constexpr int GPD = D / 64;
+    constexpr int NC = D / 16;
+    const int kvh = blockIdx.y;
+    const int j = threadIdx.x & 3, ts = threadIdx.x >> 2;
+    const int n_sl = (L + 63) / 64;
+    const int64_t hb = (int64_t)kvh * gph;          // the kv head's first group
+    const uint8_t *hw = kw + hb * 32;
+    const float *hs = ks + hb, *hbi = kb + hb;
+    // this lane's q values, q[c*16 + 4j + m]
+    float qv[NC][4];
+    const float *qh = q + (int64_t)kvh * D;
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int m = 0; m < 4; m++) qv[c][m] = qh[c * 16 + 4 * j + m];
+
+    auto compute = [&](const KQuad<D> &T, int sl) {
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // chunks c = 4*grp + 2*nib + half in order
+#pragma unroll
+        for (int grp = 0; grp < GPD; grp++)
+#pragma unroll
+            for (int nib = 0; nib < 2; nib++)
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const int c = 4 * grp + 2 * nib + half;
+                    const uint32_t x = T.w[2 * grp + half];
+                    const uint32_t n = (nib ? x >> 4 : x) & 0x0f0f0f0fu;
+                    const float s = T.sc[grp], b = T.bi[grp];
+                    a[0] = fmaf(fmaf(ubyte_f32<0>(n), s, b), qv[c][0], a[0]);
+                    a[1] = fmaf(fmaf(ubyte_f32<1>(n), s, b), qv[c][1], a[1]);
+                    a[2] = fmaf(fmaf(ubyte_f32<2>(n), s, b), qv[c][2], a[2]);
+                    a[3] = fmaf(fmaf(ubyte_f32<3>(n), s, b), qv[c][3], a[3]);
+                }
+        float v8[4], v4[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) v8[m] = __fadd_rn(a[m], quad_xor2(a[m]));
+#pragma unroll
+        for (int m = 0; m < 4; m++) v4[m] = __fadd_rn(v8[m], quad_xor1(v8[m]));
+        const float v1 = __fadd_rn(__fadd_rn(v4[0], v4[2]), __fadd_rn(v4[1], v4[3]));
+        const int t = sl * 64 + ts;
+        if (j == 0 && t < L) scores[(int64_t)kvh * L + t] = __fmul_rn(v1, rs);
+    };
+
+    // as k_score_body: kMhaBufs buffers in turn, the loads past the last
+    // slice unconditional (0, no memory traffic)
+    const int G = gridDim.x;
+    KQuad<D> buf[kMhaBufs];
+    int sl = blockIdx.x;
+#pragma unroll
+    for (int i = 0; i < kMhaBufs - 1; i++) kq_load<D>(hw, hs, hbi, L, sl + i * G, ts, j, buf[i]);
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < kMhaBufs; i++) {
+            kq_load<D>(hw, hs, hbi, L, sl + (kMhaBufs - 1) * G, ts, j,
+                       buf[(i + kMhaBufs - 1) % kMhaBufs]);
+            compute(buf[i], sl);
+            sl += G;
+            if (sl >= n_sl) return;
+        }
+    }
 }
 
 // Blocks per kv head: two waves per SIMD over the chip, at most one per
@@ -243,9 +371,18 @@ extern "C" int eakvd_k_score(const eakvd_geom *g, const uint8_t *base,
     const Planes p = planes_of(*g, base, layer, 0);
     const hipStream_t st = (hipStream_t)stream;
     const int qpk = n_q / n_kv;
-    const int kb = k_blocks(ceil_div_i(seq_len, 256), n_kv);
-    const dim3 grid((unsigned)kb, (unsigned)n_kv, (unsigned)k_head_parts(qpk, kb, n_kv));
     const float rs = 1.0f / sqrtf((float)g->head_dim);
+    const int kb = k_blocks(ceil_div_i(seq_len, 256), n_kv);
+    if (qpk == 1 && (int64_t)n_kv * kb < (int64_t)kKsBlocksPerCU * cu_count()) {
+        // MHA on a grid of 256-token slices that leaves the chip unfilled:
+        // four lanes per token, 64-token slices
+        const dim3 grid((unsigned)k_blocks(ceil_div_i(seq_len, 64), n_kv), (unsigned)n_kv);
+        auto kern = g->head_dim == 64 ? k_score_mha4_kernel<64> : k_score_mha4_kernel<128>;
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, p.w, p.s, p.b, g->gph, seq_len, q,
+                           scores, rs);
+        return (int)hipGetLastError();
+    }
+    const dim3 grid((unsigned)kb, (unsigned)n_kv, (unsigned)k_head_parts(qpk, kb, n_kv));
     auto kern = g->head_dim == 64 ? (qpk == 1 ? k_score_mha_kernel<64> : k_score_kernel<64>)
                                   : (qpk == 1 ? k_score_mha_kernel<128> : k_score_kernel<128>);
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, p.w, p.s, p.b, g->gph, seq_len, q, qpk,
