@@ -41,9 +41,14 @@ int eakv_attention_scores_device(const eakv_cache_t *c, const float *d_q,
     int prev;
     rc = eakvi_enter(c, &prev);
     if (rc) return rc;
-    int e = eakvd_k_score(&c->geom, c->dev, layer, c->seq_len, d_q, n_q, n_kv,
-                          d_scores, eakvi_stream_or_default(c, stream));
-    if (e) rc = eakvi_hip_fail(e, "k_score launch");
+    void *st = eakvi_stream_or_default(c, stream);
+    /* a caller's stream: after the cache's work pending on the shared stream */
+    rc = eakvi_order_before((eakv_cache_t *)c, st);
+    if (rc == EAKV_OK) {
+        int e = eakvd_k_score(&c->geom, c->dev, layer, c->seq_len, d_q, n_q, n_kv,
+                              d_scores, st);
+        if (e) rc = eakvi_hip_fail(e, "k_score launch");
+    }
     eakvi_leave(prev);
     return rc;
 }

@@ -354,9 +354,14 @@ int eakv_cache_load_raw_device(eakv_cache_t *c, const float *d_data,
         return eakvi_set_error(EAKV_ERR_INVALID, "load_raw: seq_len > max_seq_len");
     int prev, rc = eakvi_enter(c, &prev);
     if (rc) return rc;
-    rc = quant_rows(c, d_data, (int64_t)seq_len * c->head_dim, 0,
-                    2 * c->n_layers, seq_len, 0,
-                    eakvi_stream_or_default(c, stream));
+    void *st = eakvi_stream_or_default(c, stream);
+    /* a caller's stream: after the cache's work pending on the shared
+     * stream, and that stream's (and the host calls') later work after it */
+    rc = eakvi_order_before(c, st);
+    if (rc == EAKV_OK)
+        rc = quant_rows(c, d_data, (int64_t)seq_len * c->head_dim, 0,
+                        2 * c->n_layers, seq_len, 0, st);
+    if (rc == EAKV_OK) rc = eakvi_order_after(&c, 1, st);
     if (rc == EAKV_OK) c->seq_len = seq_len;
     eakvi_leave(prev);
     return rc;
@@ -411,9 +416,13 @@ int eakv_cache_append_device(eakv_cache_t *c, const float *d_data, int layer,
     int prev;
     rc = eakvi_enter(c, &prev);
     if (rc) return rc;
-    rc = quant_rows(c, d_data, (int64_t)n_tokens * c->head_dim,
-                    layer * 2 + kv_idx, 1, n_tokens, c->seq_len,
-                    eakvi_stream_or_default(c, stream));
+    void *st = eakvi_stream_or_default(c, stream);
+    /* as load_raw_device */
+    rc = eakvi_order_before(c, st);
+    if (rc == EAKV_OK)
+        rc = quant_rows(c, d_data, (int64_t)n_tokens * c->head_dim,
+                        layer * 2 + kv_idx, 1, n_tokens, c->seq_len, st);
+    if (rc == EAKV_OK) rc = eakvi_order_after(&c, 1, st);
     eakvi_leave(prev);
     return rc;
 }

@@ -25,9 +25,14 @@ int eakv_dequantize_range_device(const eakv_cache_t *c, int layer, int kv_idx,
         return eakvi_set_error(EAKV_ERR_INVALID, "dequantize_range: invalid argument");
     int prev, rc = eakvi_enter(c, &prev);
     if (rc) return rc;
-    int e = eakvd_dequantize(&c->geom, c->dev, layer, kv_idx, group_start, group_count,
-                             d_out, eakvi_stream_or_default(c, stream));
-    if (e) rc = eakvi_hip_fail(e, "dequantize_range");
+    void *st = eakvi_stream_or_default(c, stream);
+    /* a caller's stream: after the cache's work pending on the shared stream */
+    rc = eakvi_order_before((eakv_cache_t *)c, st);
+    if (rc == EAKV_OK) {
+        int e = eakvd_dequantize(&c->geom, c->dev, layer, kv_idx, group_start, group_count,
+                                 d_out, st);
+        if (e) rc = eakvi_hip_fail(e, "dequantize_range");
+    }
     eakvi_leave(prev);
     return rc;
 }

@@ -22,12 +22,16 @@
  * stream of the cache's own, after the device-pointer work still pending for
  * that cache on the shared stream, and wait for that stream alone: calls on
  * distinct caches from distinct threads do not wait for one another (the
- * reference's "thread-safe for distinct caches", include/eakv.h:3).  Calls
- * on one cache that use its device workspace (V-sum and fused partials, host
- * staging) are ordered among themselves whatever their streams (an event
- * recorded on a caller's stream, waited for by the next use); any other
- * ordering between caller streams (e.g. K/V appended on one caller's stream
- * and read on another) is the caller's, as for any work on two streams.
+ * reference's "thread-safe for distinct caches", include/eakv.h:3).  A
+ * device-pointer call on a caller's stream first waits, on the device, for
+ * the work pending for its caches on the shared stream; after a load or an
+ * append on a caller's stream, the shared stream's later work and the
+ * cache's later host-pointer calls wait for it.  Calls on one cache that use
+ * its device workspace (V-sum and fused partials, host staging) are ordered
+ * among themselves whatever their streams (an event recorded on a caller's
+ * stream, waited for by the next use).  Any other ordering between two
+ * caller streams (e.g. K/V appended on one caller's stream and read on
+ * another) is the caller's, as for any work on two streams.
  */
 #ifndef EAKV_HIP_H
 #define EAKV_HIP_H
