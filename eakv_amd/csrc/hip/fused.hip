@@ -1631,6 +1631,26 @@ int mfma_split(int qpk)
     return 0;
 }
 
+int per_cu_of(int d, int hh)
+{
+    return d == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
+                   : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
+}
+
+// mfma_split, and for groups of 5-8 q heads whose two-quad grid leaves more
+// than half of the chip's resident blocks idle (short contexts, few kv
+// heads): two virtual kv heads of one quad each, whose waves carry half the
+// arithmetic (each reads the kv head's tiles, the second time from L2).
+// 32Q/4KV d64 at 4096 tokens: 64 two-quad blocks become 128 one-quad blocks.
+int mfma_split_fill(int qpk, int d, int ml, int64_t units)
+{
+    const int sp = mfma_split(qpk);
+    if (sp != 1 || qpk <= 4 || qpk % 2) return sp;
+    const int per_cu = per_cu_of(d, 2);
+    const int64_t blocks = units * mfma_blocks_per_unit(ml, (int)units, per_cu);
+    return 2 * blocks < (int64_t)cu_count() * per_cu ? 2 : 1;
+}
+
 int max_len(const eakvd_batch *b)
 {
     int mx = 0;
@@ -1680,14 +1700,12 @@ FusedPlan fused_plan(const eakvd_geom *g, const eakvd_batch *b, int n_q, int n_k
     // the MFMA program addresses a layer's K and V blocks with 32-bit buffer
     // offsets
     const bool small_planes = 2 * g->block_bytes <= (int64_t)0x7fffffff;
-    p.split = mfma_split(qpk);
+    p.split = mfma_split_fill(qpk, g->head_dim, ml, (int64_t)b->n_seq * n_kv);
     p.mfma = p.split > 0 && small_planes;
     if (p.mfma) {
         p.qv = qpk / p.split;
         p.hh = p.qv <= 4 ? 1 : 2;
-        const int per_cu = g->head_dim == 64
-                               ? (p.hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
-                               : (p.hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
+        const int per_cu = per_cu_of(g->head_dim, p.hh);
         p.wpb = p.hh == 1 ? kWavesH<1> : kWavesH<2>;
         p.mc = mfma_blocks_per_unit(ml, b->n_seq * n_kv * p.split, per_cu);
         p.tt = tile_tokens(p.hh, ml, p.mc, p.wpb);
@@ -1849,7 +1867,7 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
                                 void *work, void *stream)
 {
     const int qpk = n_q / n_kv;
-    const int split = qpk < 2 ? 0 : mfma_split(qpk);
+    const int split = qpk < 2 ? 0 : mfma_split_fill(qpk, g->head_dim, seq_len, n_kv);
     if (split == 0 || 2 * g->block_bytes > (int64_t)0x7fffffff ||
         (int64_t)qpk * seq_len * 4 > (int64_t)0x7fffffff || seq_len <= 0)
         return -1;
@@ -1861,8 +1879,7 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
     b.base[0] = base;
     b.seq_len[0] = seq_len;
     const int hh = qv <= 4 ? 1 : 2;
-    const int per_cu = g->head_dim == 64 ? (hh == 1 ? kBlocksPerCUH<64, 1> : kBlocksPerCUH<64, 2>)
-                                         : (hh == 1 ? kBlocksPerCUH<128, 1> : kBlocksPerCUH<128, 2>);
+    const int per_cu = per_cu_of(g->head_dim, hh);
     const int wpb = hh == 1 ? kWavesH<1> : kWavesH<2>;
     const int mc = mfma_blocks_per_unit(seq_len, n_kv * split, per_cu);
     const int tt = tile_tokens(hh, seq_len, mc, wpb);
