@@ -1424,9 +1424,9 @@ __global__ __launch_bounds__(256) void vsum_merge_kernel(int stride, int n_chunk
 
 constexpr int kChunkV = 512;      // tokens per block
 // the MFMA program's chunks hold at least kChunkM tokens (the partials'
-// workspace is sized by it): 8 tiles, 2 per wave of a 4-wave block
+// workspace is sized by it): 4 tiles, 1 per wave of a 4-wave block
 // (mfma_blocks_per_unit)
-constexpr int kChunkM = 256;
+constexpr int kChunkM = 128;
 constexpr int kHeadsLds = 16;     // q heads per pass
 
 template <int D>
@@ -1604,18 +1604,22 @@ __global__ __launch_bounds__(D) void combine_kernel(
 // Blocks per (sequence, kv head) of the MFMA program: enough that the grid
 // fills every CU with kBlocksPerCU resident blocks once (a second, partial
 // round of blocks would idle most of the chip), and at least one.  A chunk
-// holds at least 2*kChunkM tokens (4 tiles per wave), unless that leaves
+// holds at least 4*kChunkM tokens (4 tiles per wave), unless that leaves
 // fewer blocks than CUs (short contexts, few kv heads): then kChunkM, the
-// workspace's granularity.  Measured: 8Q/8KV at 2048 tokens 11.7 -> 10.5 us
-// and 32Q/4KV d64 at 4096 10.3 -> 9.6 us with the finer chunks, but
-// 32Q/32KV at 8192 15.0 -> 17.5 us with them everywhere.
+// workspace's granularity, as long as a unit keeps at most kInBatch chunks
+// (merged in the launch), else 2*kChunkM.  Measured: 8Q/8KV at 2048 tokens
+// 11.7 -> 10.5 us and 32Q/4KV d64 at 4096 10.3 -> 9.6 us with 256-token
+// chunks, but 32Q/32KV at 8192 15.0 -> 17.5 us with them everywhere; 8Q/8KV
+// at 2048 tokens 6.86 -> 6.31 us with 128-token chunks (one tile per wave).
 int mfma_blocks_per_unit(int ml, int units, int per_cu)
 {
     const int n_cu = cu_count();
     const int slots = n_cu * per_cu;
     int nb = units >= slots ? 1 : slots / units;
-    const int coarse = (ml + 2 * kChunkM - 1) / (2 * kChunkM);
-    const int cap = (int64_t)units * coarse < n_cu ? (ml + kChunkM - 1) / kChunkM : coarse;
+    const int coarse = (ml + 4 * kChunkM - 1) / (4 * kChunkM);
+    int fine = (ml + kChunkM - 1) / kChunkM;
+    if (fine > kInBatch) fine = max(kInBatch, (ml + 2 * kChunkM - 1) / (2 * kChunkM));
+    const int cap = (int64_t)units * coarse < n_cu ? fine : coarse;
     nb = nb < cap ? nb : cap;
     return nb < 1 ? 1 : nb;
 }
