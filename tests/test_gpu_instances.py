@@ -10,9 +10,8 @@ every compiled form of the kernel meets the reference bar
 (fused_attention.ea:190-373) at least once, with both entry points giving
 the same bits.  The same six forms in V-sum mode (the unfused output call
 for 2-8 q heads per kv head) are held to the oracle's V-sum.  The 70B-shape
-and headline launches (test_gpu_headline)
-cover d=128 with two quads and 64-token tiles, and d=128 with one quad, at
-their own shapes.
+and headline launches (test_gpu_headline) cover d=128 with two quads and
+64-token tiles, and d=128 with one quad, at their own shapes.
 """
 import numpy as np
 import pytest
