@@ -630,8 +630,8 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // Quad hq holds heads 4hq..4hq+3.  Rows of heads >= G are zero (their q
     // is read from head 0 and dropped).  Every wave of the block serves the
     // same heads, so wave hq alone computes quad hq's operands and shares
-    // them through LDS.  The q loads are issued first, then the first two
-    // load groups (further below), so the digit arithmetic waits only for q.
+    // them through LDS.  The q loads are issued first, then the first load
+    // groups (further below), so the digit arithmetic waits only for q.
     const int ha = (l & 15) >> 2, pa = l & 3, qq = l >> 4;
     bool qrow[HH];
     float qv[HH][GPD][16];
@@ -760,8 +760,9 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         __builtin_amdgcn_sched_barrier(0);
     };
     // Unconditional (a wave without tiles reads the unit's last tile), so
-    // the waits below count the same younger loads on every path.  Group 0
-    // has no V tile; in its place one 256-byte load of tile T(0)'s V bytes
+    // the waits below count the same younger loads on every path.  One quad
+    // per wave: group 1 follows at once; two quads: once group 0 has landed
+    // (after the q digits, below).  Group 0 has no V tile; in its place one 256-byte load of tile T(0)'s V bytes
     // (fetched again by group 1, so no extra memory traffic) goes to the V
     // slot that iteration 0 fills.  It makes the prologue load every V slot
     // in the loop's order, which keeps the compiler's wait placement at the
@@ -776,7 +777,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     if constexpr (VS) load_w<D, HH, TT>(st[0], wr, wo, ldt(tk[0]), tl, L);
     else load_k<D, TT>(st[0], P, ldt(tk[0]), oob(tk[0]));
     __builtin_amdgcn_sched_barrier(0);
-    load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
+    if constexpr (HH == 1) load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
 
     // scores are kept in the log2 domain (times log2(e))
     const float rs2 = rs * EAKV_LOG2E;
@@ -866,6 +867,19 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
         }
         // every wave has its operands before any wave writes digit rows
         __syncthreads();
+    }
+
+    // Two quads: group 1 once group 0 has landed.  Every wave of the chip
+    // issues its first group at the start; holding the second back until the
+    // first is in lets the first groups arrive first, so waves start on their
+    // first tiles sooner and leave the start in step less (64Q/8KV d128:
+    // 34.1 against 35.35 us per call at 131072 tokens, 13.25 against 13.95
+    // at 20000).  One-quad waves, with half the arithmetic per tile, gained
+    // nothing at 32Q/8KV 32K x 8 and lost 0.25 us at 32Q/4KV d64 4K (two
+    // tiles per wave).
+    if constexpr (HH == 2) {
+        wait_vm<0>();
+        load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
     }
 
     WaveState<D> S[HH];
