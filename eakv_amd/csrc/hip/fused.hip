@@ -762,11 +762,12 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // Unconditional (a wave without tiles reads the unit's last tile), so
     // the waits below count the same younger loads on every path.  One quad
     // per wave: group 1 follows at once; two quads: once group 0 has landed
-    // (after the q digits, below).  Group 0 has no V tile; in its place one 256-byte load of tile T(0)'s V bytes
-    // (fetched again by group 1, so no extra memory traffic) goes to the V
-    // slot that iteration 0 fills.  It makes the prologue load every V slot
-    // in the loop's order, which keeps the compiler's wait placement at the
-    // loop head as tight as inside the loop.
+    // (after the q digits, below).  Group 0 has no V tile; in its place one
+    // 256-byte load of tile T(0)'s V bytes (fetched again by group 1, so no
+    // extra memory traffic) goes to the V slot that iteration 0 fills.  It
+    // makes the prologue load every V slot in the loop's order, which keeps
+    // the compiler's wait placement at the loop head as tight as inside the
+    // loop.
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         P.vw, (lds_ptr)vslot(std::integral_constant<int, kSlots - 1>{}), 4,
         (int)(P.vwo + oob(tk[0])),
