@@ -347,14 +347,18 @@ def slope_case(E, rng, d, n_q, n_kv, L, slope, center):
 
 @pytest.mark.parametrize("d,n_q,n_kv,L,slope", [
     (128, 32, 8, 600, 0.2), (128, 64, 8, 600, 0.25), (128, 64, 8, 96, 1.5),
-    (64, 8, 8, 1500, 0.05), (128, 16, 4, 700, -0.2), (64, 32, 4, 90, 1.4)])
+    (64, 8, 8, 1500, 0.05), (128, 16, 4, 700, -0.2), (64, 32, 4, 90, 1.4),
+    (128, 64, 8, 20000, 0.007), (64, 64, 8, 16400, -0.008)])
 def test_fused_rising_and_falling_scores(E, rng, d, n_q, n_kv, L, slope):
     """Scores within about +-150: rising ones move the running max again and
     again (every tile at the steep slopes, in every quad of q heads); falling
-    ones put the max in the first tile and drive the later weights to 0."""
+    ones put the max in the first tile and drive the later weights to 0.  The
+    long contexts run two-quad waves (8 q heads per wave), asserted."""
     say("fused-slope", d, n_q, n_kv, L, slope)
     g, o, q, smax = slope_case(E, rng, d, n_q, n_kv, L, slope, center=True)
     assert smax < 160
+    if L > 10000:
+        assert E.fused_plan([g], n_q, n_kv)["quads"] == 2
     a = g.attention_fused(q, 0, n_q, n_kv)
     b = o.attention_fused(q, 0, n_q, n_kv)
     assert np.isfinite(a).all()
@@ -395,7 +399,8 @@ def test_fused_huge_scores_as_accurate_as_reference(E, rng, d, n_q, n_kv, L, slo
 
 
 @pytest.mark.parametrize("d,n_q,n_kv,L,where", [(128, 32, 8, 700, "k"), (128, 16, 2, 300, "v"),
-                                                (64, 8, 4, 500, "k"), (128, 64, 8, 450, "v")])
+                                                (64, 8, 4, 500, "k"), (128, 64, 8, 450, "v"),
+                                                (128, 64, 8, 20000, "k"), (64, 64, 8, 16400, "v")])
 def test_fused_nonfinite_cache_values_propagate(E, rng, d, n_q, n_kv, L, where):
     """A NaN as the first value of a 64-value group quantizes to a NaN scale
     and bias (the strict min/max scan keeps it).  In K it makes that token's
@@ -409,6 +414,8 @@ def test_fused_nonfinite_cache_values_propagate(E, rng, d, n_q, n_kv, L, where):
     g.load_raw(data, L)
     o.load_raw(data, L)
     q = rng.standard_normal((n_q, d)).astype(np.float32)
+    if L > 10000:                               # two-quad waves
+        assert E.fused_plan([g], n_q, n_kv)["quads"] == 2
     a = g.attention_fused(q, 0, n_q, n_kv)
     b = o.attention_fused(q, 0, n_q, n_kv)
     nan = np.isnan(b)
