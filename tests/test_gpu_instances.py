@@ -37,6 +37,8 @@ CASES = [
     (64, 64, 8, [16400] * 7 + [9001], 2, 64),
     # two quads, d=128, 4 sequences: 8 chunks per unit, 64-token tiles
     (128, 64, 8, [16400, 16400, 16400, 16399], 2, 64),
+    # the same launch with ragged contexts: one token, a third of the tiles
+    (128, 64, 8, [16400, 1, 5555, 16399], 2, 64),
 ]
 
 
