@@ -572,7 +572,7 @@ template <int D, int HH, bool VS, int TT>
 __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, HH> / 4)) void mfma_kernel(
     eakvd_geom g, eakvd_batch bt, int layer, const float *__restrict__ q,
     int n_q, int qpk, float rs, float *__restrict__ part, int split,
-    float *__restrict__ out, uint8_t *__restrict__ ctr)
+    float *__restrict__ out, uint8_t *__restrict__ ctr, int lead)
 {
     constexpr int GPD = D / 64;
     constexpr int NK = Geo<D, TT>::NK;
@@ -1117,6 +1117,20 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     constexpr int kGrp = Geo<D, TT>::NVD + kDma<D, TT> + NKL;   // loads per group
     constexpr int kLater = (kSlots - 1) * kGrp;         // loads of the groups after the oldest
     constexpr int kEarly = (kSlots - 2) * kGrp;
+    // lead > 0 (one-quad waves): the grid holds two blocks per CU, dealt one per CU in each
+    // of two dispatch rounds (blocks in linear order), and on each SIMD the
+    // older wave wins issue, so the first round's blocks would run ahead
+    // and the second's finish alone at half the CU's rate.  The second
+    // round's waves issue first for their first `lead` tiles (half of
+    // them), then give way.  Priority changes no arithmetic.
+    int lead_left = 0;
+    if constexpr (HH == 1)
+        if (lead > 0 &&
+            2 * (int)((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) >=
+                (int)(gridDim.x * gridDim.y * gridDim.z)) {
+            lead_left = lead;
+            __builtin_amdgcn_s_setprio(1);
+        }
     if (tk[0] < n_tiles) {
         {
             Scales<D, TT> C;
@@ -1152,6 +1166,8 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             }
 #pragma unroll
             for (int j = 0; j < kSlots; j++) tk[j] = __builtin_amdgcn_readfirstlane(tk[j + 1]);
+            if constexpr (HH == 1)
+                if (lead_left > 0 && --lead_left == 0) __builtin_amdgcn_s_setprio(0);
             return more;
         };
         // The explicit waits above count the loads of every group in issue
@@ -1828,8 +1844,18 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         auto kern = mfma_entry<false>(g->head_dim, hh, p.tt);
         const int64_t units = (int64_t)n_kv * p.split * b->n_seq;
         uint8_t *uc = merge_in_launch(g, ctr, mc, units) ? (uint8_t *)ctr : nullptr;
+        // one-quad grids of exactly two rounds of one block per CU: the
+        // second round leads for half of its tiles (32Q/8KV d128 32K x 8:
+        // 55.24-55.30 against 55.55-55.96 us per layer step, alternating
+        // whole bench runs)
+        int lead = 0;
+        if (hh == 1 && units * mc == 2 * (int64_t)cu_count()) {
+            const int64_t n_tiles = ((int64_t)max_len(b) + p.tt - 1) / p.tt;
+            const int64_t waves = (int64_t)mc * wpb;
+            lead = (int)(((n_tiles + waves - 1) / waves + 1) / 2);
+        }
         hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, *b, layer, q, n_q, p.qv, rs,
-                           part, p.split, out, uc);
+                           part, p.split, out, uc, lead);
         if (uc) return (int)hipGetLastError();
         const int tt = p.tt;
         if (parts && g->head_dim == 64)
@@ -1909,7 +1935,7 @@ extern "C" int eakvd_v_sum_mfma(const eakvd_geom *g, const uint8_t *base, int la
     uint8_t *ctr = const_cast<uint8_t *>(base) + g->ctr_off;
     uint8_t *uc = merge_in_launch(g, ctr, mc, units) ? ctr : nullptr;
     hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), 0, st, *g, b, layer, w, n_q, qv, 0.0f,
-                       part, split, out, uc);
+                       part, split, out, uc, 0);
     if (uc) return (int)hipGetLastError();
     // the chunks that hold a partial: blocks with a tile (see mfma_kernel)
     const int n_tiles = (seq_len + tt - 1) / tt;
