@@ -878,6 +878,18 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     // at 20000).  One-quad waves, with half the arithmetic per tile, gained
     // nothing at 32Q/8KV 32K x 8 and lost 0.25 us at 32Q/4KV d64 4K (two
     // tiles per wave).
+    // Two quads (8-wave blocks, 2 waves per SIMD): waves 4-7 share their
+    // SIMDs with the older waves 0-3 and lead them for the first half of
+    // their own tiles, as the second round of one-quad blocks does below
+    // (64Q/8KV d128 128K: 34.16-34.18 against 34.73-34.75 us per call,
+    // alternating whole bench runs).  Set before group 1, so that group's
+    // block runs on into the first wait that counts it.
+    int lead_left = 0;
+    if constexpr (HH == 2)
+        if (w >= NW / 2) {
+            lead_left = ((n_tiles - first + stride - 1) / stride + 1) / 2;
+            if (lead_left > 0) __builtin_amdgcn_s_setprio(1);
+        }
     if constexpr (HH == 2) {
         wait_vm<0>();
         load_group(std::integral_constant<int, 1>{}, tk[0], tk[1]);
@@ -1117,13 +1129,12 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
     constexpr int kGrp = Geo<D, TT>::NVD + kDma<D, TT> + NKL;   // loads per group
     constexpr int kLater = (kSlots - 1) * kGrp;         // loads of the groups after the oldest
     constexpr int kEarly = (kSlots - 2) * kGrp;
-    // lead > 0 (one-quad waves): the grid holds two blocks per CU, dealt one per CU in each
-    // of two dispatch rounds (blocks in linear order), and on each SIMD the
-    // older wave wins issue, so the first round's blocks would run ahead
-    // and the second's finish alone at half the CU's rate.  The second
-    // round's waves issue first for their first `lead` tiles (half of
+    // lead > 0 (one-quad waves): the grid holds two blocks per CU, dealt one
+    // per CU in each of two dispatch rounds (blocks in linear order), and on
+    // each SIMD the older wave wins issue, so the first round's blocks would
+    // run ahead and the second's finish alone at half the CU's rate.  The
+    // second round's waves issue first for their first `lead` tiles (half of
     // them), then give way.  Priority changes no arithmetic.
-    int lead_left = 0;
     if constexpr (HH == 1)
         if (lead > 0 &&
             2 * (int)((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) >=
@@ -1166,8 +1177,7 @@ __global__ __launch_bounds__(64 * kWavesH<HH>, (kWavesH<HH> * kBlocksPerCUH<D, H
             }
 #pragma unroll
             for (int j = 0; j < kSlots; j++) tk[j] = __builtin_amdgcn_readfirstlane(tk[j + 1]);
-            if constexpr (HH == 1)
-                if (lead_left > 0 && --lead_left == 0) __builtin_amdgcn_s_setprio(0);
+            if (lead_left > 0 && --lead_left == 0) __builtin_amdgcn_s_setprio(0);
             return more;
         };
         // The explicit waits above count the loads of every group in issue
