@@ -1856,8 +1856,9 @@ extern "C" int eakvd_fused(const eakvd_geom *g, const eakvd_batch *b,
         uint8_t *uc = merge_in_launch(g, ctr, mc, units) ? (uint8_t *)ctr : nullptr;
         // one-quad grids of exactly two rounds of one block per CU: the
         // second round leads for half of its tiles (32Q/8KV d128 32K x 8:
-        // 55.24-55.30 against 55.55-55.96 us per layer step, alternating
-        // whole bench runs)
+        // 54.48-54.51 against 55.07-55.13 us per layer step, alternating
+        // whole bench runs on one box; 55.24-55.30 against 55.55-55.96 on
+        // another)
         int lead = 0;
         if (hh == 1 && units * mc == 2 * (int64_t)cu_count()) {
             const int64_t n_tiles = ((int64_t)max_len(b) + p.tt - 1) / p.tt;
