@@ -121,19 +121,35 @@ static inline int cu_count()
 
 // ---- Q4 group quantization pieces shared by the cache quantizer and the
 // ggml block type (8 lanes per 64-value group).
-
-// f32 -> i32 with x86 cvttss2si semantics (NaN / out of range -> INT32_MIN).
-__device__ __forceinline__ int to_i32_x86(float v)
+//
+// The reference's nibble is q = clamp(to_i32((x - mn)*inv + 0.5), 0, 15),
+// each step rounded, to_i32 with x86 cvttss2si semantics (NaN and values
+// outside the int32 range -> INT32_MIN), inv = range > 0 ? 15/range : 0.
+// Over the values a group can produce, one v_cvt_i32_f32 (truncation, NaN
+// -> 0) gives the same nibble:
+//   inv finite and > 0: every non-NaN element lies in [mn, mx], so x - mn
+//     rounds into [0, range] and (x - mn)*inv to at most
+//     RN(range * RN(15/range)) <= 15 + 2^-20; v lies in [0.5, 16) and
+//     truncates to 0..15 with the clamp idle.  A NaN element gives v = NaN
+//     -> 0, the reference's INT32_MIN clamped.
+//   inv = 0 (range 0, NaN or +inf): v = 0.5 or NaN -> 0, as the reference.
+//   inv = +inf (15/range overflows: range < 15/FLT_MAX): the reference's v
+//     is +inf (x > mn) or NaN (x = mn: 0*inf), every nibble 0.  q4_factor
+//     turns that inv into NaN, so every v is NaN -> 0.
+// (The range test and clamp cost three more instructions per element.)
+__device__ __forceinline__ float q4_factor(float inv)
 {
-    return (v >= -2147483648.0f && v < 2147483648.0f) ? (int)v : (int)0x80000000;
+    return inv == __builtin_inff() ? __builtin_nanf("") : inv;
 }
 
-// q(x) = clamp(to_i32((x - mn)*inv + 0.5), 0, 15), each step rounded.
-__device__ __forceinline__ uint32_t q4(float x, float mn, float inv)
+// q4(x, mn, q4_factor(inv)): the reference's nibble of x.
+__device__ __forceinline__ uint32_t q4(float x, float mn, float f)
 {
-    float v = __fadd_rn(__fmul_rn(__fsub_rn(x, mn), inv), 0.5f);
-    int q = to_i32_x86(v);
-    q = q < 0 ? 0 : (q > 15 ? 15 : q);
+    const float v = __fadd_rn(__fmul_rn(__fsub_rn(x, mn), f), 0.5f);
+    int q;
+    // the instruction itself, whose NaN result is defined (0), where C's
+    // float-to-int conversion leaves NaN undefined
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(v));
     return (uint32_t)q;
 }
 

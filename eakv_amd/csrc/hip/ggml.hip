@@ -13,14 +13,18 @@ namespace {
 // scan of ggml_type.c:79-85; d = range/15 (0 for a constant block),
 // id = range > 0 ? 15/range : 0, q = clamp(trunc(0.5 + (x - min)*id), 0, 15)
 // (ggml_type.c:47-50, :79-87); byte k = q(x[k]) | q(x[k+32]) << 4.  Each
-// lane loads its next block before it quantizes the current one.
+// lane loads its next block before it quantizes the current one.  Loads and
+// stores are non-temporal, each byte being touched once (65,536 rows of 4096:
+// 199.6-200.3 against 221.4-222.9 us per call with the default policy).
 template <bool VEC>
 __device__ __forceinline__ void load_block8(const float *bp, int l8, float4 &lo, float4 &hi)
 {
     const float *a = bp + l8 * 4, *c = bp + 32 + l8 * 4;
     if (VEC) {
-        lo = *reinterpret_cast<const float4 *>(a);
-        hi = *reinterpret_cast<const float4 *>(c);
+        const v4f x = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(a));
+        const v4f y = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(c));
+        lo = make_float4(x[0], x[1], x[2], x[3]);
+        hi = make_float4(y[0], y[1], y[2], y[3]);
     } else {
         lo = make_float4(a[0], a[1], a[2], a[3]);
         hi = make_float4(c[0], c[1], c[2], c[3]);
@@ -47,15 +51,17 @@ __global__ __launch_bounds__(256) void ggml_quantize_kernel(const float *__restr
         const float range = __fsub_rn(mx, mn);
         const float d = range / 15.0f;
         const float id = range > 0.0f ? 15.0f / range : 0.0f;
-        const uint32_t b0 = q4(lo.x, mn, id) | (q4(hi.x, mn, id) << 4);
-        const uint32_t b1 = q4(lo.y, mn, id) | (q4(hi.y, mn, id) << 4);
-        const uint32_t b2 = q4(lo.z, mn, id) | (q4(hi.z, mn, id) << 4);
-        const uint32_t b3 = q4(lo.w, mn, id) | (q4(hi.w, mn, id) << 4);
+        const float f = q4_factor(id);
+        const uint32_t b0 = q4(lo.x, mn, f) | (q4(hi.x, mn, f) << 4);
+        const uint32_t b1 = q4(lo.y, mn, f) | (q4(hi.y, mn, f) << 4);
+        const uint32_t b2 = q4(lo.z, mn, f) | (q4(hi.z, mn, f) << 4);
+        const uint32_t b3 = q4(lo.w, mn, f) | (q4(hi.w, mn, f) << 4);
         uint8_t *blk = dst + b * 40;
-        *reinterpret_cast<uint32_t *>(blk + l8 * 4) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        __builtin_nontemporal_store(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24),
+                                    reinterpret_cast<uint32_t *>(blk + l8 * 4));
         if (l8 == 0) {
-            *reinterpret_cast<float *>(blk + 32) = d;
-            *reinterpret_cast<float *>(blk + 36) = mn;
+            __builtin_nontemporal_store(d, reinterpret_cast<float *>(blk + 32));
+            __builtin_nontemporal_store(mn, reinterpret_cast<float *>(blk + 36));
         }
         b = bn;
         lo = nlo;
@@ -90,8 +96,12 @@ __global__ __launch_bounds__(256) void ggml_dequantize_kernel(const uint8_t *__r
         hi.w = fmaf((float)(x >> 28), d, m);
         float *o = dst + b * 64;
         if (VEC) {
-            reinterpret_cast<float4 *>(o)[i] = lo;
-            reinterpret_cast<float4 *>(o)[8 + i] = hi;
+            // non-temporal: 1 GiB of f32 out, 199.6-201.7 against
+            // 264.9-269.7 us per call (65,536 rows of 4096) with the default
+            // policy
+            __builtin_nontemporal_store(v4f{lo.x, lo.y, lo.z, lo.w}, reinterpret_cast<v4f *>(o) + i);
+            __builtin_nontemporal_store(v4f{hi.x, hi.y, hi.z, hi.w},
+                                        reinterpret_cast<v4f *>(o) + 8 + i);
         } else {
             o[4 * i] = lo.x; o[4 * i + 1] = lo.y; o[4 * i + 2] = lo.z; o[4 * i + 3] = lo.w;
             o[32 + 4 * i] = hi.x; o[33 + 4 * i] = hi.y; o[34 + 4 * i] = hi.z;
