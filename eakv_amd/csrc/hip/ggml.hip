@@ -126,6 +126,9 @@ __global__ __launch_bounds__(256) void ggml_vec_dot_kernel(int nb, float *s, siz
         const uint8_t *x = vx + r * bx;
         const float *y = reinterpret_cast<const float *>(vy + r * by);
         float acc = 0.0f;
+        // four blocks' loads in flight (65,536 rows of 4096: 215.9-217.2
+        // against 229.6-229.8 us per call; eight: 222.4-222.9)
+#pragma unroll 4
         for (int i = 0; i < nb; i++) {
             const uint8_t *blk = x + (int64_t)i * 40;
             const float d = *reinterpret_cast<const float *>(blk + 32);
