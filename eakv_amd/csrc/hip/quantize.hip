@@ -7,9 +7,10 @@
 //            min = max = NaN)
 //   scale  = range > 0 ? range/15 : 1,  inv = range > 0 ? 15/range : 0
 //   bias   = min
-//   q(x)   = clamp(to_i32((x - min)*inv + 0.5), 0, 15), two roundings,
+//   q(x)   = clamp(to_i32((x - min)*inv + 0.5), 0, 15), each step rounded,
 //            to_i32 with x86 cvttss2si semantics (NaN / out of range ->
-//            INT32_MIN, then clamped to 0)
+//            INT32_MIN, then clamped to 0); one v_cvt_i32_f32 gives the same
+//            nibble for every value a group can produce (q4, common.h)
 //   byte k = q(x[k+32])*16 + q(x[k])
 //
 // Work split: 8 lanes per group; lane j holds elements 4j..4j+3 (its four
@@ -52,8 +53,8 @@ __device__ __forceinline__ QOut quantize_group8(const float4 &lo, const float4 &
     return o;
 }
 
-// Every source and output byte is touched once: loads and stores are
-// non-temporal (64Q/8KV d128 128K rows, 537 MB of f32 per launch from
+// Every source and output byte is touched once: the 16-byte loads of aligned
+// rows and the stores are non-temporal (64Q/8KV d128 128K rows, 537 MB of f32 per launch from
 // HBM: 102.7-103.0 against 107.0-108.1 us per launch with the default
 // policy and one group per lane; 32Q/8KV d128 32K rows: 29.4-29.5 against
 // 31.1-31.5 us).
