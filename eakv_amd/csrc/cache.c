@@ -150,6 +150,21 @@ int eakvi_host_begin(eakv_cache_t *c)
     return eakvi_order_before(c, c->hstream);
 }
 
+int eakvi_pinned(eakv_cache_t *c, size_t n, void **p)
+{
+    if (n > c->pin_bytes) {
+        /* nothing in flight uses the old buffer: every use ends in a wait */
+        if (c->pin) eakvd_host_free(c->pin);
+        c->pin = NULL;
+        c->pin_bytes = 0;
+        int e = eakvd_host_malloc(&c->pin, n);
+        if (e) return eakvi_hip_fail(e, "pinned host scratch");
+        c->pin_bytes = n;
+    }
+    *p = c->pin;
+    return EAKV_OK;
+}
+
 int eakvi_host_end(eakv_cache_t *c, int rc, int used_work, const char *what)
 {
     int e = eakvd_stream_sync(c->hstream);
@@ -277,6 +292,7 @@ void eakv_cache_free(eakv_cache_t *c)
     if (c->order_event) eakvd_event_destroy(c->order_event);
     if (c->hstream) eakvd_stream_destroy(c->hstream);
     if (c->work) eakvd_free(c->work);
+    if (c->pin) eakvd_host_free(c->pin);
     if (c->dev) eakvd_free(c->dev);
     if (ok) eakvi_leave(prev);
     free(c);

@@ -78,13 +78,10 @@ int eakv_validate(const eakv_cache_t *cc, int32_t *results)
     const int64_t n = (int64_t)c->n_kv_heads * c->head_dim * c->seq_len / 64;
     int prev, rc = eakvi_enter(c, &prev);
     if (rc) return rc;
-    unsigned long long *h = malloc((size_t)nb * sizeof(*h));
-    if (!h) {
-        eakvi_leave(prev);
-        return eakvi_set_error(EAKV_ERR_ALLOC, "validate: out of host memory");
-    }
+    unsigned long long *h = NULL;
     void *st = c->hstream;
     rc = eakvi_host_begin(c);
+    if (rc == EAKV_OK) rc = eakvi_pinned(c, (size_t)nb * sizeof(*h), (void **)&h);
     if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, (size_t)nb * sizeof(*h));
     const int began = rc == EAKV_OK;
     if (began) {
@@ -95,7 +92,6 @@ int eakv_validate(const eakv_cache_t *cc, int32_t *results)
     rc = eakvi_host_end(c, rc, began, "validate");
     if (rc == EAKV_OK)
         for (int i = 0; i < nb; i++) results[i] = h[i] == ~0ull ? 0 : (int32_t)(h[i] & 3);
-    free(h);
     eakvi_leave(prev);
     return rc;
 }

@@ -32,6 +32,8 @@ struct eakv_cache {
     void  *work;           /* device scratch for staging and partials */
     size_t work_bytes;
     void  *work_event;     /* recorded after a use of `work` on a caller's stream */
+    void  *pin;            /* pinned host scratch for small results copied back */
+    size_t pin_bytes;
     int    work_on_caller; /* the last use of `work` was on a caller's stream */
     void  *order_event;    /* orders a batched call against this cache's stream */
     unsigned own_async;    /* device-pointer calls enqueued on `stream` so far */
@@ -83,5 +85,10 @@ void *eakvi_batch_stream(eakv_cache_t *const *caches, int n, void *s);
  * their own work only.  Returns rc, or the wait's error if rc is EAKV_OK. */
 int  eakvi_host_begin(eakv_cache_t *c);
 int  eakvi_host_end(eakv_cache_t *c, int rc, int used_work, const char *what);
+
+/* The cache's pinned host scratch, at least n bytes (grown on demand; the
+ * device's copies into pinned memory skip the runtime's staging of pageable
+ * memory).  Used between eakvi_host_begin and eakvi_host_end only. */
+int  eakvi_pinned(eakv_cache_t *c, size_t n, void **p);
 
 #endif
