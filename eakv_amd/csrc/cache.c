@@ -158,11 +158,11 @@ int eakvi_pinned(eakv_cache_t *c, size_t n, void **p)
         c->pin = NULL;
         c->pin_bytes = 0;
         int e = eakvd_host_malloc(&c->pin, n);
-        if (e) return eakvi_hip_fail(e, "pinned host scratch");
+        if (e) return e;
         c->pin_bytes = n;
     }
     *p = c->pin;
-    return EAKV_OK;
+    return 0;
 }
 
 int eakvi_host_end(eakv_cache_t *c, int rc, int used_work, const char *what)

@@ -22,7 +22,10 @@ int eakvd_free(void *p) { return p ? (int)hipFree(p) : 0; }
 int eakvd_host_malloc(void **p, size_t n)
 {
     *p = nullptr;
-    return (int)hipHostMalloc(p, n, hipHostMallocDefault);
+    const hipError_t e = hipHostMalloc(p, n, hipHostMallocDefault);
+    // the launchers report hipGetLastError(): leave no failure behind for them
+    if (e != hipSuccess) (void)hipGetLastError();
+    return (int)e;
 }
 
 int eakvd_host_free(void *p) { return p ? (int)hipHostFree(p) : 0; }

@@ -81,7 +81,10 @@ int eakv_validate(const eakv_cache_t *cc, int32_t *results)
     unsigned long long *h = NULL;
     void *st = c->hstream;
     rc = eakvi_host_begin(c);
-    if (rc == EAKV_OK) rc = eakvi_pinned(c, (size_t)nb * sizeof(*h), (void **)&h);
+    if (rc == EAKV_OK) {
+        int e = eakvi_pinned(c, (size_t)nb * sizeof(*h), (void **)&h);
+        if (e) rc = eakvi_hip_fail(e, "validate: pinned host scratch");
+    }
     if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, (size_t)nb * sizeof(*h));
     const int began = rc == EAKV_OK;
     if (began) {

@@ -87,8 +87,9 @@ int  eakvi_host_begin(eakv_cache_t *c);
 int  eakvi_host_end(eakv_cache_t *c, int rc, int used_work, const char *what);
 
 /* The cache's pinned host scratch, at least n bytes (grown on demand; the
- * device's copies into pinned memory skip the runtime's staging of pageable
- * memory).  Used between eakvi_host_begin and eakvi_host_end only. */
+ * device's copies from and into pinned memory skip the runtime's staging of
+ * pageable memory).  Used between eakvi_host_begin and eakvi_host_end only.
+ * Returns 0 or the HIP error of the allocation (the error text untouched). */
 int  eakvi_pinned(eakv_cache_t *c, size_t n, void **p);
 
 #endif
