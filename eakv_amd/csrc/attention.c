@@ -28,49 +28,6 @@ static int attn_check(const eakv_cache_t *c, int layer, int n_q, int n_kv)
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-/* Host buffers of a synchronous call, up to kPinMax bytes in all, travel
- * through the cache's pinned host scratch: the input is copied in and sent
- * from there, the result lands there and is copied out after the call's
- * wait.  The runtime's own staging of pageable memory costs more per copy
- * (8 heads, d=128, one layer: the host-pointer V-sum 27.2-27.3 against
- * 34.8-35.0 us per call at 2048 tokens and 36.1-36.2 against 45.1-45.2 at
- * 8192; the K-score 37.1-37.5 against 39.4-39.6 at 8192).  Larger buffers,
- * or no pinned memory, go from and to pageable memory directly. */
-#define kPinMax ((size_t)4 << 20)
-
-typedef struct {
-    char  *pin;       /* NULL: pageable copies */
-    size_t out_off;   /* the result's offset in pin */
-} bounce_t;
-
-static void bounce_begin(eakv_cache_t *c, size_t in_b, size_t out_b, bounce_t *bo)
-{
-    void *p = NULL;
-    bo->out_off = align256(in_b);
-    bo->pin = bo->out_off + out_b <= kPinMax &&
-                      eakvi_pinned(c, bo->out_off + out_b, &p) == 0
-                  ? (char *)p : NULL;
-}
-
-static int bounce_in(const bounce_t *bo, void *d_dst, const void *src, size_t n, void *st)
-{
-    if (!n) return 0;
-    if (!bo->pin) return eakvd_memcpy_h2d_async(d_dst, src, n, st);
-    memcpy(bo->pin, src, n);
-    return eakvd_memcpy_h2d_async(d_dst, bo->pin, n, st);
-}
-
-static int bounce_out(const bounce_t *bo, void *dst, const void *d_src, size_t n, void *st)
-{
-    if (!n) return 0;
-    return eakvd_memcpy_d2h_async(bo->pin ? bo->pin + bo->out_off : dst, d_src, n, st);
-}
-
-/* after the call's wait */
-static void bounce_end(const bounce_t *bo, int rc, void *dst, size_t n)
-{
-    if (rc == EAKV_OK && bo->pin && n) memcpy(dst, bo->pin + bo->out_off, n);
-}
 
 /* ------------------------------------------------------------------------ */
 /* K-score                                                                   */
@@ -116,19 +73,19 @@ void eakv_attention_scores(const eakv_cache_t *cc, const float *queries,
     int rc = eakvi_host_begin(c);
     if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, align256(qb) + sb);
     const int began = rc == EAKV_OK;
-    bounce_t bo = {NULL, 0};
+    eakvi_bounce bo = {NULL, 0};
     if (began) {
         float *dq = (float *)c->work;
         float *ds = (float *)((char *)c->work + align256(qb));
-        bounce_begin(c, qb, sb, &bo);
-        int e = bounce_in(&bo, dq, queries, qb, st);
+        eakvi_bounce_begin(c, qb, sb, &bo);
+        int e = eakvi_bounce_in(&bo, dq, queries, qb, st);
         if (!e) e = eakvd_k_score(&c->geom, c->dev, layer, c->seq_len, dq, n_q,
                                   n_kv, ds, st);
-        if (!e) e = bounce_out(&bo, scores_out, ds, sb, st);
+        if (!e) e = eakvi_bounce_out(&bo, scores_out, ds, sb, st);
         if (e) rc = eakvi_hip_fail(e, "attention_scores");
     }
     rc = eakvi_host_end(c, rc, began, "attention_scores");
-    bounce_end(&bo, rc, scores_out, sb);
+    eakvi_bounce_end(&bo, rc, scores_out, sb);
     eakvi_leave(prev);
 }
 
@@ -183,20 +140,20 @@ void eakv_attention_output(const eakv_cache_t *cc, const float *weights,
     int rc = eakvi_host_begin(c);
     if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, align256(wb) + align256(ob) + pb);
     const int began = rc == EAKV_OK;
-    bounce_t bo = {NULL, 0};
+    eakvi_bounce bo = {NULL, 0};
     if (began) {
         float *dw = (float *)c->work;
         float *dout = (float *)((char *)c->work + align256(wb));
         void *part = (char *)c->work + align256(wb) + align256(ob);
-        bounce_begin(c, wb, ob, &bo);
-        int e = bounce_in(&bo, dw, weights, wb, st);
+        eakvi_bounce_begin(c, wb, ob, &bo);
+        int e = eakvi_bounce_in(&bo, dw, weights, wb, st);
         if (!e) e = eakvd_v_sum(&c->geom, c->dev, layer, c->seq_len, dw, n_q,
                                 n_kv, dout, part, st);
-        if (!e) e = bounce_out(&bo, output_out, dout, ob, st);
+        if (!e) e = eakvi_bounce_out(&bo, output_out, dout, ob, st);
         if (e) rc = eakvi_hip_fail(e, "attention_output");
     }
     rc = eakvi_host_end(c, rc, began, "attention_output");
-    bounce_end(&bo, rc, output_out, ob);
+    eakvi_bounce_end(&bo, rc, output_out, ob);
     eakvi_leave(prev);
 }
 
@@ -289,18 +246,18 @@ int eakv_attention_fused(const eakv_cache_t *cc, const float *queries,
     if (rc == EAKV_OK) rc = eakvi_work_begin(c, st, 2 * io + pb);
     const int began = rc == EAKV_OK;
     const size_t qb = (size_t)n_q * c->head_dim * 4;
-    bounce_t bo = {NULL, 0};
+    eakvi_bounce bo = {NULL, 0};
     if (began) {
         float *dq = (float *)c->work;
         float *dout = (float *)((char *)c->work + io);
-        bounce_begin(c, qb, qb, &bo);
-        int e = bounce_in(&bo, dq, queries, qb, st);
+        eakvi_bounce_begin(c, qb, qb, &bo);
+        int e = eakvi_bounce_in(&bo, dq, queries, qb, st);
         if (!e) e = fused_launch(&c, 1, layer, dq, n_q, n_kv, dout, st);
-        if (!e) e = bounce_out(&bo, output_out, dout, qb, st);
+        if (!e) e = eakvi_bounce_out(&bo, output_out, dout, qb, st);
         if (e) rc = eakvi_hip_fail(e, "attention_fused");
     }
     rc = eakvi_host_end(c, rc, began, "attention_fused");
-    bounce_end(&bo, rc, output_out, qb);
+    eakvi_bounce_end(&bo, rc, output_out, qb);
     eakvi_leave(prev);
     return rc;
 }

@@ -92,4 +92,18 @@ int  eakvi_host_end(eakv_cache_t *c, int rc, int used_work, const char *what);
  * Returns 0 or the HIP error of the allocation (the error text untouched). */
 int  eakvi_pinned(eakv_cache_t *c, size_t n, void **p);
 
+/* A host-pointer call's input and result through the pinned scratch when
+ * they fit (pin NULL: pageable copies).  begin reserves in_b + out_b bytes;
+ * in and out enqueue the copies on st; end copies the result out once the
+ * call's wait has succeeded (rc). */
+typedef struct {
+    char  *pin;
+    size_t out_off;
+} eakvi_bounce;
+void eakvi_bounce_begin(eakv_cache_t *c, size_t in_b, size_t out_b, eakvi_bounce *bo);
+int  eakvi_bounce_in(const eakvi_bounce *bo, void *d_dst, const void *src, size_t n, void *st);
+int  eakvi_bounce_out(const eakvi_bounce *bo, void *dst, const void *d_src, size_t n,
+                      void *st);
+void eakvi_bounce_end(const eakvi_bounce *bo, int rc, void *dst, size_t n);
+
 #endif
