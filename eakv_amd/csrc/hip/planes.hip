@@ -104,12 +104,6 @@ __global__ __launch_bounds__(256) void validate_kernel(const uint8_t *__restrict
     }
 }
 
-int grid_for(int64_t threads)
-{
-    int64_t b = (threads + 255) / 256;
-    return (int)(b < 1 ? 1 : b > 4096 ? 4096 : b);
-}
-
 }  // namespace
 
 extern "C" int eakvd_dequantize(const eakvd_geom *g, const uint8_t *base, int layer, int kv,
@@ -135,7 +129,11 @@ extern "C" int eakvd_validate(const eakvd_geom *g, const uint8_t *base, int n_bl
                                   (hipStream_t)stream);
     if (e != hipSuccess) return (int)e;
     if (n <= 0 || n_blocks <= 0) return 0;
-    const int gx = grid_for((n + 3) / 4) < 64 ? grid_for((n + 3) / 4) : 64;
+    // one pass over a block's groups (up to 1024 x 256 lanes of four groups;
+    // the 64 blocks of a 32K cache: 39.0-39.6 against 40.4-40.8 us with 64
+    // blocks per row walking eight steps)
+    const int64_t nbx = ((n + 3) / 4 + 255) / 256;
+    const int gx = (int)(nbx < 1 ? 1 : nbx > 1024 ? 1024 : nbx);
     hipLaunchKernelGGL(validate_kernel, dim3(gx, n_blocks), dim3(256), 0, (hipStream_t)stream,
                        base, g->block_bytes, g->s_off, g->b_off, n, res);
     return (int)hipGetLastError();
